@@ -1,0 +1,168 @@
+"""Benchmark of the fused recurrence on one MI355X (driver contract: one JSON line).
+
+Workload (the north-star metric): LSTM, B=8, T=1024,
+N=3 heads, D=256, BF16 tensors, BF16-operand / FP32-state recurrence, forward
+plus backward to all four inputs (Wx, R, b, initial state). A "step" is one
+``flashrnn()`` forward and one ``torch.autograd.grad`` over synthetic inputs
+already resident in HBM: Wx ~ N(0,1), R ~ N(0,1/D), b ~ N(0,0.1^2), zero
+initial state, upstream cotangents ~ N(0,1) on states and last state.
+
+Reported: ``value`` = timesteps*batch / s over the timed steps; ``roofline``
+for the dominant kernel (its average launch duration from HIP events recorded
+by libfrnn around each launch inside the timed region, against MI355X dense
+BF16 MFMA peak); ``cpu_baseline`` = the CPU oracle (restated flashrnn_torch,
+numerics fp32_state_bf16_mma) on the same shape on this host's cores.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+METRIC = "fwd+bwd timesteps·batch/s, LSTM B8 T1024 N3 D256 bf16; % MFMA peak"
+B, T, N, D, G, S = 8, 1024, 3, 256, 4, 2
+PEAK_BF16_TFLOPS = 2500.0  # MI355X dense BF16 MFMA
+FLOP_PER_LAUNCH = 2.0 * B * T * N * G * D * D  # one recurrent product (fwd), R^T dG (bwd) or dR GEMM
+MI355X_CUS = 256
+
+
+def make_inputs(torch, device, seed=20261201):
+    g = torch.Generator().manual_seed(seed)
+    wx = torch.randn(B, T, G, N, D, generator=g)
+    R = torch.randn(G, N, D, D, generator=g) / D**0.5
+    b = 0.1 * torch.randn(G, N, D, generator=g)
+    s0 = torch.zeros(S, B, 1, N, D)
+    dh = torch.randn(S, B, T, N, D, generator=g)
+    dl = torch.randn(S, B, 1, N, D, generator=g)
+    return (wx, R, b, s0), (dh, dl)
+
+
+def cpu_baseline(torch, budget_s=30.0):
+    """The CPU oracle at the full workload shape: median of up to 3 fwd+bwd runs."""
+    from oracle.torch_restatement import flashrnn_torch
+
+    cores = min(16, os.cpu_count() or 1)
+    torch.set_num_threads(cores)
+    (wx, R, b, s0), (dh, dl) = make_inputs(torch, "cpu")
+    leaves = [t.bfloat16().float().requires_grad_() for t in (wx, R, b, s0)]
+    # warm-up on a short prefix
+    h, l = flashrnn_torch(leaves[0][:, :16], *leaves[1:], cell="lstm", numerics="fp32_state_bf16_mma")
+    torch.autograd.grad(h.sum() + l.sum(), leaves)
+    times = []
+    t_start = time.perf_counter()
+    while len(times) < 3 and time.perf_counter() - t_start < budget_s:
+        t0 = time.perf_counter()
+        h, l = flashrnn_torch(*leaves, cell="lstm", numerics="fp32_state_bf16_mma")
+        torch.autograd.grad((h * dh).sum() + (l * dl).sum(), leaves)
+        times.append(time.perf_counter() - t0)
+    times.sort()
+    med = times[len(times) // 2]
+    return {
+        "value": B * T / med,
+        "unit": "timesteps*batch/s",
+        "cores": cores,
+        "kind": "port",
+        "sample": f"full workload shape (B8 T1024 N3 D256 LSTM fwd+bwd), FP32 CPU oracle "
+        f"(restated flashrnn_torch, numerics=fp32_state_bf16_mma), median of {len(times)} runs "
+        f"({', '.join(f'{t:.2f}s' for t in times)})",
+    }
+
+
+def main(argv=None):
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=30)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args(argv)
+    if args.gpus != 1:
+        print(
+            f"bench.py measures one GPU only: the recurrence shards over heads/batch with no per-step "
+            f"exchange (see DESIGN.md), and this build runs on single-GPU boxes; got --gpus {args.gpus}",
+            file=sys.stderr,
+        )
+        return 2
+
+    import torch
+
+    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+    from flashrnn_amd import _lib, flashrnn, synchronize_and_check
+
+    dev = torch.device("cuda", 0)
+    (wx, R, b, s0), (dh, dl) = make_inputs(torch, dev)
+    leaves = [t.to(dev, torch.bfloat16).requires_grad_() for t in (wx, R, b, s0)]
+    dh = dh.to(dev, torch.bfloat16)
+    dl = dl.to(dev, torch.bfloat16)
+
+    def step():
+        h, last = flashrnn(leaves[0], leaves[1], leaves[2], leaves[3], function="lstm", dtype="bfloat16")
+        return torch.autograd.grad((h, last), leaves, grad_outputs=(dh, dl))
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    synchronize_and_check()
+
+    lib = _lib.load()
+    lib.frnn_timing_enable(1)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    lib.frnn_timing_enable(0)
+    ms, cnt = _lib.timing_read()
+    synchronize_and_check()
+
+    ms_per_step = (t1 - t0) * 1e3 / args.steps
+    value = B * T / (ms_per_step / 1e3)
+    names = ["forward recurrence", "backward recurrence", "dR GEMM + reduction"]
+    avg = [m / c if c else 0.0 for m, c in zip(ms, cnt)]
+    dom = max(range(3), key=lambda k: avg[k])
+    achieved = FLOP_PER_LAUNCH / (avg[dom] / 1e3) / 1e12
+    # CUs the persistent kernels occupy: one per workgroup (N heads x D/16 tiles)
+    cus = N * (D // 16)
+    result = {
+        "metric": METRIC,
+        "value": round(value, 1),
+        "unit": "timesteps*batch/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded normal inputs, zero initial state)",
+        "config": {
+            "workload": "LSTM fwd+bwd, B8 T1024 N3 D256 (BASELINE configs[1])",
+            "cell": "lstm", "batch": B, "seq_len": T, "heads": N, "head_dim": D,
+            "numerics": "bf16 MFMA operands, fp32 accumulate and state",
+            "parallelism": "single GPU",
+        },
+        "kernels_ms": {n: round(a, 4) for n, a in zip(names, avg)},
+        "roofline": {
+            "bound": "mfma",
+            "kernel": names[dom],
+            "achieved": round(achieved, 3),
+            "peak": PEAK_BF16_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(achieved / PEAK_BF16_TFLOPS, 6),
+            "active_cu_frac": round(achieved / (PEAK_BF16_TFLOPS * cus / MI355X_CUS), 5),
+            "flop_per_launch": FLOP_PER_LAUNCH,
+            "traffic": None,
+        },
+    }
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline(torch)
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

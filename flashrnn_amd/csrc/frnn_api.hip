@@ -1,0 +1,373 @@
+// C ABI of libfrnn.so: validation, launch plan, workspace layout, launches.
+// Replaces FlashRNNFuncFused (flashrnn/flashrnn/fused/flashrnn.cc:244-535)
+// and ForwardPass/BackwardPass::Run (fused/flashrnn_fused_forward.cu:773-976,
+// fused/flashrnn_fused_backward.cu:769-1087). See include/frnn.h.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <atomic>
+#include <cstring>
+#include <mutex>
+#include <vector>
+
+#include "../../include/frnn.h"
+#include "frnn_kernels.h"
+#include "frnn_plan.h"
+
+namespace {
+
+using frnn::Plan;
+
+std::atomic<uint32_t> g_spin_limit{1u << 22};
+
+// ---- optional kernel timing (frnn_timing_enable / frnn_timing_read)
+struct Timing {
+  std::mutex mu;
+  bool on = false;
+  std::vector<hipEvent_t> free_events;
+  struct Rec { int kind; hipEvent_t a, b; };
+  std::vector<Rec> pending;
+  hipEvent_t get() {
+    if (!free_events.empty()) {
+      hipEvent_t e = free_events.back();
+      free_events.pop_back();
+      return e;
+    }
+    hipEvent_t e = nullptr;
+    if (hipEventCreate(&e) != hipSuccess) return nullptr;
+    return e;
+  }
+};
+Timing g_timing;
+
+// Record the start event of a timed region; returns false when timing is off.
+bool timing_begin(hipStream_t st, hipEvent_t* a) {
+  std::lock_guard<std::mutex> lk(g_timing.mu);
+  if (!g_timing.on) return false;
+  *a = g_timing.get();
+  return *a && hipEventRecord(*a, st) == hipSuccess;
+}
+void timing_end(int kind, hipEvent_t a, hipStream_t st) {
+  std::lock_guard<std::mutex> lk(g_timing.mu);
+  hipEvent_t b = g_timing.get();
+  if (!b || hipEventRecord(b, st) != hipSuccess) return;
+  g_timing.pending.push_back({kind, a, b});
+}
+
+constexpr long long kAlign = 256;
+long long align_up(long long x) { return (x + kAlign - 1) / kAlign * kAlign; }
+
+bool cell_sizes(int cell, int* gr, int* gw, int* gt, int* s) {
+  switch (cell) {
+    case FRNN_LSTM: *gr = 4; *gw = 4; *gt = 4; *s = 2; return true;
+    case FRNN_GRU: *gr = 3; *gw = 3; *gt = 4; *s = 1; return true;
+    case FRNN_ELMAN: *gr = 1; *gw = 1; *gt = 1; *s = 1; return true;
+    case FRNN_SLSTM: *gr = 4; *gw = 4; *gt = 4; *s = 4; return true;
+  }
+  return false;
+}
+
+int nsave_of(int cell) {
+  switch (cell) {
+    case FRNN_LSTM: return 6;
+    case FRNN_GRU: return 5;
+    case FRNN_ELMAN: return 1;
+    case FRNN_SLSTM: return 11;
+  }
+  return 0;
+}
+
+// Smallest built k-tiles-per-wave class that holds `need`.
+int ktw_class(int need) {
+  for (int c : {1, 2, 4, 6, 8})
+    if (need <= c) return c;
+  return 0;
+}
+
+int make_plan(const frnn_desc* d, Plan* p) {
+  if (!d) return FRNN_E_INVALID;
+  std::memset(p, 0, sizeof(*p));
+  if (!cell_sizes(d->cell, &p->GR, &p->GW, &p->GT, &p->S)) return FRNN_E_INVALID;
+  if (d->batch < 1 || d->steps < 1 || d->heads < 1 || d->width < 1) return FRNN_E_INVALID;
+  if (d->dtype_io != FRNN_F32 && d->dtype_io != FRNN_BF16) return FRNN_E_INVALID;
+  if (d->dtype_state != FRNN_F32 && d->dtype_state != FRNN_BF16) return FRNN_E_INVALID;
+  if (d->mma != FRNN_MMA_BF16 && d->mma != FRNN_MMA_F32) return FRNN_E_INVALID;
+  if (d->width % 32 != 0 || d->width > 1024) return FRNN_E_UNSUPPORTED;
+  p->cell = d->cell;
+  p->B = d->batch;
+  p->T = d->steps;
+  p->N = d->heads;
+  p->D = d->width;
+  p->mma = d->mma;
+  p->dt_io = d->dtype_io;
+  p->dt_state = d->dtype_state;
+  p->flags = d->flags;
+  p->NB = 1;
+  p->BS = 16 * p->NB;
+  p->nslab = (p->B + p->BS - 1) / p->BS;
+  p->Bp8 = (p->B + 7) / 8 * 8;
+  p->ngroups = p->N * p->nslab;
+    p->kt_fwd = p->D / 32;
+  p->kt_bwd = p->GR * p->D / 32;
+  const int KT = p->kt_fwd;
+  // hidden tiles per workgroup: a group must fit the 32 CUs of one XCD
+  p->NDT = (p->D / 16 <= 32) ? 1 : 2;
+  // contraction split: more waves per tile shorten the per-step MFMA chain;
+  // the workgroup stays at <= 8 waves (256 VGPRs per lane available)
+  const int max_ks = 8 / p->NDT;
+  p->KS = std::min(std::min(4, max_ks), KT);
+  if (p->mma == FRNN_MMA_F32) p->KS = std::min(max_ks, KT);
+  int need = (KT + p->KS - 1) / p->KS;
+  if (!ktw_class(need)) return FRNN_E_UNSUPPORTED;
+  // registers per lane held by the resident R^T and the dG fragments of the backward
+  const int frag_vgprs = p->mma == FRNN_MMA_BF16 ? 4 : 8;
+  if (2 * p->GR * ktw_class(need) * frag_vgprs > 200) return FRNN_E_UNSUPPORTED;
+  p->epl = (4 * p->NB + p->KS - 1) / p->KS;
+  p->nsave = nsave_of(p->cell);
+  p->wpg = p->D / (16 * p->NDT);
+  p->grid = (p->flags & FRNN_XCD_SHARED) ? p->ngroups * p->wpg
+                                         : frnn::kXcds * p->wpg * ((p->ngroups + frnn::kXcds - 1) / frnn::kXcds);
+  p->nwg = p->ngroups * p->wpg;
+  const long long wsz = p->mma == FRNN_MMA_BF16 ? 4 : 8;
+  p->xwords_fwd = (long long)p->ngroups * p->BS * p->D;
+  p->xwords_bwd = (long long)p->ngroups * p->BS * p->GR * p->D;
+  p->save_floats = (long long)p->T * p->nwg * p->nsave * p->NDT * p->KS * 64 * p->epl;
+  const long long KC = (long long)p->T * (p->Bp8 / 8);
+  p->hsave_elems = (long long)p->N * KC * p->D * 8;
+  p->dgsave_elems = (long long)p->N * KC * p->GR * p->D * 8;
+  // dR GEMM split: aim for ~4096 waves, at least 8 k-tiles per split
+  const long long tiles = (long long)p->N * (p->GR * p->D / 32) * (p->D / 32);
+  const long long ktt = (KC + 3) / 4;
+  long long split = std::max<long long>(1, 4096 / std::max<long long>(1, tiles));
+  split = std::min<long long>(split, std::max<long long>(1, ktt / 8));
+  p->splitk = (int)std::min<long long>(split, 64);
+  // saved-for-backward area
+  const long long gsz = p->mma == FRNN_MMA_BF16 ? 2 : 4;  // dR-GEMM operand element
+  p->off_save_h = align_up(p->save_floats * 4);
+  p->save_bytes = align_up(p->off_save_h + p->hsave_elems * gsz);
+  // workspaces: status word at 0, exchange at 256
+  p->off_x = kAlign;
+  p->ws_fwd = align_up(p->off_x + 2 * p->xwords_fwd * wsz);
+  p->off_save_dg = align_up(p->off_x + 2 * p->xwords_bwd * wsz);
+  p->off_part = align_up(p->off_save_dg + p->dgsave_elems * gsz);
+  p->off_dbpart = align_up(p->off_part + (long long)p->splitk * p->N * p->GR * p->D * p->D * 4);
+  p->ws_bwd = align_up(p->off_dbpart + (long long)p->ngroups * p->GT * p->BS * p->D * 4);
+  if (2 * p->xwords_bwd * wsz > 0x7fffffffLL) return FRNN_E_UNSUPPORTED;  // buffer-descriptor range
+  return FRNN_OK;
+}
+
+int launch(const void* fn, int grid, int block, size_t lds, void* arg, hipStream_t stream) {
+  void* args[] = {arg};
+  if (hipLaunchKernel(fn, dim3(grid), dim3(block), args, lds, stream) != hipSuccess) {
+    (void)hipGetLastError();  // do not leave the error to the caller's next HIP call
+    return FRNN_E_LAUNCH;
+  }
+  return FRNN_OK;
+}
+
+// The persistent kernels need every active workgroup of a group resident at
+// once. Check that the busiest XCD (or, placement-free, the GPU) can hold them.
+int check_residency(const Plan& p, const void* fn, int block, size_t lds) {
+  int dev = 0, cus = 0, per_cu = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return FRNN_E_LAUNCH;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return FRNN_E_LAUNCH;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, block, lds) != hipSuccess) {
+    (void)hipGetLastError();
+    return FRNN_E_LAUNCH;
+  }
+  long long need, have;
+  if (p.flags & FRNN_XCD_SHARED) {
+    need = (long long)p.ngroups * p.wpg;
+    have = (long long)cus * per_cu;
+  } else {
+    need = (long long)((p.ngroups + frnn::kXcds - 1) / frnn::kXcds) * p.wpg;
+    have = (long long)(cus / frnn::kXcds) * per_cu;
+  }
+  return need <= have ? FRNN_OK : FRNN_E_UNSUPPORTED;
+}
+
+int clear(void* base, long long bytes, hipStream_t stream) {
+  uint32_t* p = static_cast<uint32_t*>(base);
+  long n = (long)(bytes / 4);
+  if (n <= 0) return FRNN_OK;
+  int grid = (int)std::min<long>(1024, (n + 255) / 256);
+  struct {
+    uint32_t* p;
+    long n;
+  } a{p, n};
+  void* args[] = {&a.p, &a.n};
+  return hipLaunchKernel(frnn::zero_kernel(), dim3(grid), dim3(256), args, 0, stream) == hipSuccess
+             ? FRNN_OK
+             : FRNN_E_LAUNCH;
+}
+
+}  // namespace
+
+extern "C" {
+
+int frnn_cell_sizes(int cell, int32_t* g_r, int32_t* g_w, int32_t* g_t, int32_t* s) {
+  int a, b, c, e;
+  if (!cell_sizes(cell, &a, &b, &c, &e)) return FRNN_E_INVALID;
+  if (g_r) *g_r = a;
+  if (g_w) *g_w = b;
+  if (g_t) *g_t = c;
+  if (s) *s = e;
+  return FRNN_OK;
+}
+
+size_t frnn_workspace_bytes(const frnn_desc* d, int which) {
+  Plan p;
+  if (make_plan(d, &p) != FRNN_OK) return 0;
+  switch (which) {
+    case 0: return (size_t)p.ws_fwd;
+    case 1: return (size_t)p.ws_bwd;
+    case 2: return (size_t)p.save_bytes;
+  }
+  return 0;
+}
+
+int frnn_fwd(const frnn_desc* d, const void* wx, const void* R, const void* b, const void* s0,
+             void* states_out, void* carry_out, void* save, void* ws, size_t ws_bytes,
+             frnn_stream_t stream) {
+  Plan p;
+  int rc = make_plan(d, &p);
+  if (rc != FRNN_OK) return rc;
+  if (!wx || !R || !b || !s0 || !states_out || !ws) return FRNN_E_INVALID;
+  const bool training = (p.flags & FRNN_TRAINING) != 0;
+  if (training && !save) return FRNN_E_INVALID;
+  if ((long long)ws_bytes < p.ws_fwd) return FRNN_E_WORKSPACE;
+  const void* fn = frnn::recurrence_kernel(p.cell, p.mma, ktw_class((p.kt_fwd + p.KS - 1) / p.KS), true);
+  if (!fn) return FRNN_E_UNSUPPORTED;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  char* w = static_cast<char*>(ws);
+  const long long xbytes = p.ws_fwd - p.off_x;
+  if ((rc = clear(w + p.off_x, xbytes, st)) != FRNN_OK) return rc;
+  frnn::FwdArgs a;
+  a.p = p;
+  a.wx = wx;
+  a.R = R;
+  a.bias = b;
+  a.s0 = s0;
+  a.states = states_out;
+  a.carry = carry_out;
+  a.save = training ? static_cast<float*>(save) : nullptr;
+  a.hsave = training ? static_cast<void*>(static_cast<char*>(save) + p.off_save_h) : nullptr;
+  a.xbuf = w + p.off_x;
+  a.xbytes = xbytes;
+  a.status = reinterpret_cast<uint32_t*>(w);
+  a.spin_limit = g_spin_limit.load();
+  const size_t lds = (size_t)2 * p.NDT * p.KS * p.NB * p.GR * 256 * sizeof(float);
+  const int block = 64 * p.NDT * p.KS;
+  if ((rc = check_residency(p, fn, block, lds)) != FRNN_OK) return rc;
+  hipEvent_t t0;
+  const bool timed = timing_begin(st, &t0);
+  rc = launch(fn, p.grid, block, lds, &a, st);
+  if (timed) timing_end(0, t0, st);
+  return rc;
+}
+
+int frnn_bwd(const frnn_desc* d, const void* R, const void* s0, const void* save, const void* d_states,
+             const void* d_carry, void* dwx, void* dR, void* db, void* ds0, void* ws, size_t ws_bytes,
+             frnn_stream_t stream) {
+  Plan p;
+  int rc = make_plan(d, &p);
+  if (rc != FRNN_OK) return rc;
+  (void)s0;
+  if (!R || !save || !dwx || !dR || !db || !ds0 || !ws) return FRNN_E_INVALID;
+  if ((long long)ws_bytes < p.ws_bwd) return FRNN_E_WORKSPACE;
+  const void* fn = frnn::recurrence_kernel(p.cell, p.mma, ktw_class((p.kt_fwd + p.KS - 1) / p.KS), false);
+  if (!fn) return FRNN_E_UNSUPPORTED;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  char* w = static_cast<char*>(ws);
+  const long long xbytes = p.off_save_dg - p.off_x;
+  if ((rc = clear(w + p.off_x, xbytes, st)) != FRNN_OK) return rc;
+  frnn::BwdArgs a;
+  a.p = p;
+  a.R = R;
+  a.save = static_cast<const float*>(save);
+  a.d_states = d_states;
+  a.d_carry = d_carry;
+  a.dwx = dwx;
+  a.ds0 = ds0;
+  a.dgsave = static_cast<void*>(w + p.off_save_dg);
+  a.dbpart = reinterpret_cast<float*>(w + p.off_dbpart);
+  a.xbuf = w + p.off_x;
+  a.xbytes = xbytes;
+  a.status = reinterpret_cast<uint32_t*>(w);
+  a.spin_limit = g_spin_limit.load();
+  const size_t lds = (size_t)2 * p.NDT * p.KS * p.NB * 256 * sizeof(float);
+  const int block = 64 * p.NDT * p.KS;
+  if ((rc = check_residency(p, fn, block, lds)) != FRNN_OK) return rc;
+  hipEvent_t t0;
+  bool timed = timing_begin(st, &t0);
+  rc = launch(fn, p.grid, block, lds, &a, st);
+  if (timed) timing_end(1, t0, st);
+  if (rc != FRNN_OK) return rc;
+
+  frnn::GemmArgs g;
+  g.p = p;
+  g.dgsave = a.dgsave;
+  g.hsave = static_cast<const void*>(static_cast<const char*>(save) + p.off_save_h);
+  g.part = reinterpret_cast<float*>(w + p.off_part);
+  g.dbpart = a.dbpart;
+  g.dR = dR;
+  g.db = db;
+  const long long waves = (long long)p.N * (p.GR * p.D / 32) * (p.D / 32) * p.splitk;
+  timed = timing_begin(st, &t0);
+  rc = launch(frnn::gemm_kernel(p.mma), (int)((waves + 3) / 4), 256, 0, &g, st);
+  const long long nout = (long long)p.N * p.GR * p.D * p.D + (long long)p.GT * p.N * p.D;
+  const int rgrid = (int)std::min<long long>(4096, (nout + 255) / 256);
+  if (rc == FRNN_OK) rc = launch(frnn::reduce_kernel(), rgrid, 256, 0, &g, st);
+  if (timed) timing_end(2, t0, st);
+  return rc;
+}
+
+int frnn_status(const void* ws, frnn_stream_t stream) {
+  if (!ws) return FRNN_E_INVALID;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  if (hipStreamSynchronize(st) != hipSuccess) return FRNN_E_LAUNCH;
+  uint32_t v = 0;
+  if (hipMemcpy(&v, ws, sizeof(v), hipMemcpyDeviceToHost) != hipSuccess) return FRNN_E_LAUNCH;
+  return v == 0 ? FRNN_OK : -(int)v;
+}
+
+const char* frnn_strerror(int code) {
+  switch (code) {
+    case FRNN_OK: return "ok";
+    case FRNN_E_INVALID: return "invalid argument (null pointer, unknown enum or non-positive size)";
+    case FRNN_E_UNSUPPORTED: return "unsupported configuration (width, register or co-residency limits)";
+    case FRNN_E_WORKSPACE: return "workspace smaller than frnn_workspace_bytes()";
+    case FRNN_E_LAUNCH: return "HIP kernel launch failed (co-residency or resources)";
+    case FRNN_E_TIMEOUT: return "recurrence exchange timed out on the device";
+    case FRNN_E_PLACEMENT: return "a workgroup ran on an unexpected XCD; retry with FRNN_XCD_SHARED";
+  }
+  return "unknown frnn error";
+}
+
+void frnn_timing_enable(int on) {
+  std::lock_guard<std::mutex> lk(g_timing.mu);
+  g_timing.on = on != 0;
+}
+
+int frnn_timing_read(double* ms3, int32_t* counts3) {
+  std::lock_guard<std::mutex> lk(g_timing.mu);
+  for (int k = 0; k < 3; ++k) {
+    if (ms3) ms3[k] = 0.0;
+    if (counts3) counts3[k] = 0;
+  }
+  int rc = FRNN_OK;
+  for (auto& r : g_timing.pending) {
+    float ms = 0.f;
+    if (hipEventSynchronize(r.b) != hipSuccess || hipEventElapsedTime(&ms, r.a, r.b) != hipSuccess) rc = FRNN_E_LAUNCH;
+    if (ms3) ms3[r.kind] += ms;
+    if (counts3) counts3[r.kind] += 1;
+    g_timing.free_events.push_back(r.a);
+    g_timing.free_events.push_back(r.b);
+  }
+  g_timing.pending.clear();
+  return rc;
+}
+
+void frnn_set_spin_limit(uint32_t polls) { g_spin_limit.store(polls ? polls : 1u); }
+
+}  // extern "C"

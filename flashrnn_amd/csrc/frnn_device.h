@@ -1,0 +1,197 @@
+// Device-side building blocks of the gfx950 fused recurrence.
+//
+// Execution model (see frnn_plan.h for the host side of the same plan):
+//  * a "group" is one head n and one batch slab of 16*NB rows; it owns the
+//    whole recurrence of that slab and never talks to another group;
+//  * a group is D/16 workgroups, one per 16-wide tile of hidden units; all of
+//    them run on one XCD (workgroup w runs on XCD w % 8), so they share an L2;
+//  * inside a workgroup, KS waves split the contraction (K) dimension of the
+//    per-step product and reduce their partial sums through LDS;
+//  * each step, every workgroup publishes its slice of the new hidden state
+//    (forward) or of the gate cotangent dG (backward) into an exchange buffer
+//    in L2 as tagged words; readers poll those words until the tag of the
+//    step arrives. That is the whole grid "barrier": no counters, no flags.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace frnn {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned short u16x8 __attribute__((ext_vector_type(8)));
+
+enum { CELL_LSTM = 0, CELL_GRU = 1, CELL_ELMAN = 2, CELL_SLSTM = 3 };
+enum { MMA_BF16 = 0, MMA_F32 = 1 };
+enum { DT_F32 = 0, DT_BF16 = 1 };
+enum { ST_OK = 0, ST_TIMEOUT = 5, ST_PLACEMENT = 6 };
+
+// Cell shapes: recurrent gates, input gates, bias gates, states.
+template <int CELL> struct CellShape;
+template <> struct CellShape<CELL_LSTM> { static constexpr int GR = 4, GW = 4, GT = 4, S = 2; };
+template <> struct CellShape<CELL_GRU> { static constexpr int GR = 3, GW = 3, GT = 4, S = 1; };
+template <> struct CellShape<CELL_ELMAN> { static constexpr int GR = 1, GW = 1, GT = 1, S = 1; };
+template <> struct CellShape<CELL_SLSTM> { static constexpr int GR = 4, GW = 4, GT = 4, S = 4; };
+
+// ------------------------------------------------------------------ numbers
+__device__ __forceinline__ uint32_t f2u(float x) { return __builtin_bit_cast(uint32_t, x); }
+__device__ __forceinline__ float u2f(uint32_t x) { return __builtin_bit_cast(float, x); }
+
+// FP32 -> BF16 bits, round to nearest even; NaN stays a (quiet) NaN.
+__device__ __forceinline__ uint32_t bf16_bits(float x) {
+  uint32_t u = f2u(x);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x40u;
+  return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+}
+__device__ __forceinline__ float bf16_to_f32(uint32_t bits) { return u2f(bits << 16); }
+__device__ __forceinline__ float round_bf16(float x) { return bf16_to_f32(bf16_bits(x)); }
+
+// Loads/stores of the public tensors in their runtime dtype.
+__device__ __forceinline__ float ld_val(const void* p, long i, int dt) {
+  if (dt == DT_F32) return static_cast<const float*>(p)[i];
+  return bf16_to_f32(static_cast<const unsigned short*>(p)[i]);
+}
+__device__ __forceinline__ void st_val(void* p, long i, int dt, float v) {
+  if (dt == DT_F32) static_cast<float*>(p)[i] = v;
+  else static_cast<unsigned short*>(p)[i] = (unsigned short)bf16_bits(v);
+}
+
+// Activations from the hardware exp2 / log2 / reciprocal (v_exp_f32,
+// v_log_f32, v_rcp_f32); formulas are the textbook ones.
+__device__ __forceinline__ float fexp(float x) { return __builtin_amdgcn_exp2f(x * 1.4426950408889634f); }
+__device__ __forceinline__ float frcp(float x) { return __builtin_amdgcn_rcpf(x); }
+__device__ __forceinline__ float sigmoidf_(float x) { return frcp(1.0f + fexp(-x)); }
+__device__ __forceinline__ float tanhf_(float x) {
+  // tanh x = 1 - 2 / (exp(2x) + 1); symmetric form keeps large |x| exact.
+  float e = fexp(2.0f * fabsf(x));
+  float r = 1.0f - 2.0f * frcp(e + 1.0f);
+  return copysignf(r, x);
+}
+__device__ __forceinline__ float logsigmoidf_(float x) {
+  // log sigma(x) = min(x, 0) - log1p(exp(-|x|))
+  float e = fexp(-fabsf(x));
+  return fminf(x, 0.0f) - __builtin_amdgcn_logf(1.0f + e) * 0.6931471805599453f;
+}
+
+// ------------------------------------------------------------------- MFMA
+// One 16x16 output tile, K = 32 per call. Both operand layouts put 8
+// consecutive logical k in each lane (lane l: row/col l%16, k-block l/16);
+// the bf16 instruction consumes that directly, the f32 path issues eight
+// 16x16x4 steps over the same k's. Output: lane l, reg i = (row 4*(l/16)+i, col l%16).
+template <int MMA> struct Frag;
+template <> struct Frag<MMA_BF16> {
+  bf16x8 v;
+  __device__ __forceinline__ void zero() { v = bf16x8{}; }
+};
+template <> struct Frag<MMA_F32> {
+  float v[8];
+  __device__ __forceinline__ void zero() {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = 0.f;
+  }
+};
+
+__device__ __forceinline__ f32x4 mma(const Frag<MMA_BF16>& a, const Frag<MMA_BF16>& b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.v, b.v, c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x4 mma(const Frag<MMA_F32>& a, const Frag<MMA_F32>& b, f32x4 c) {
+#pragma unroll
+  for (int i = 0; i < 8; ++i) c = __builtin_amdgcn_mfma_f32_16x16x4f32(a.v[i], b.v[i], c, 0, 0, 0);
+  return c;
+}
+
+// Set fragment element j from an FP32 value (rounded for the bf16 path).
+__device__ __forceinline__ void frag_set(Frag<MMA_BF16>& f, int j, float x) {
+  f.v[j] = __builtin_bit_cast(__bf16, (unsigned short)bf16_bits(x));
+}
+__device__ __forceinline__ void frag_set(Frag<MMA_F32>& f, int j, float x) { f.v[j] = x; }
+
+// ------------------------------------------------------ exchange words
+// BF16 path: 32-bit word = (tag << 16) | bf16 bits.   F32 path: 64-bit word = (tag << 32) | f32 bits.
+// Tags cycle 1,1,2,2,1,1,... so a slot (double-buffered by step parity)
+// never holds its own step's tag before the step is written, and the
+// zero-cleared buffer never matches.
+__device__ __forceinline__ uint32_t step_tag(int it) { return 1u + ((uint32_t)(it >> 1) & 1u); }
+
+template <int MMA> struct Word;
+template <> struct Word<MMA_BF16> { typedef uint32_t type; };
+template <> struct Word<MMA_F32> { typedef uint64_t type; };
+
+struct Xchg {
+  __amdgpu_buffer_rsrc_t rsrc;  // whole exchange region, for the sc1 loads
+  char* base;
+  int shared_xcd;               // 1: stores write through to memory-side coherence (sc1)
+};
+
+// Store one exchange word. Same-XCD mode uses a non-temporal store (it lands
+// in the shared L2); the placement-free mode uses an agent-scope store.
+template <int MMA>
+__device__ __forceinline__ void xstore(const Xchg& x, long word, float v, uint32_t tag) {
+  if constexpr (MMA == MMA_BF16) {
+    uint32_t w = (tag << 16) | bf16_bits(v);
+    uint32_t* p = reinterpret_cast<uint32_t*>(x.base) + word;
+    if (x.shared_xcd) __hip_atomic_store(p, w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    else __builtin_nontemporal_store(w, p);
+  } else {
+    uint64_t w = ((uint64_t)tag << 32) | f2u(v);
+    uint64_t* p = reinterpret_cast<uint64_t*>(x.base) + word;
+    if (x.shared_xcd) __hip_atomic_store(p, w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    else __builtin_nontemporal_store(w, p);
+  }
+}
+
+// Issue the loads of one 8-word run (8 consecutive k) at word index `word`.
+// sc1 (aux 16) makes the load miss the CU-local L1 and read the L2.
+template <int MMA> struct Run;
+template <> struct Run<MMA_BF16> { u32x4 q[2]; };
+template <> struct Run<MMA_F32> { u32x4 q[4]; };
+
+template <int MMA>
+__device__ __forceinline__ void xload(const Xchg& x, long word, Run<MMA>& r) {
+  constexpr int NQ = MMA == MMA_BF16 ? 2 : 4;
+  const int byte = (int)(word * (MMA == MMA_BF16 ? 4 : 8));
+#pragma unroll
+  for (int q = 0; q < NQ; ++q) r.q[q] = __builtin_amdgcn_raw_buffer_load_b128(x.rsrc, byte + 16 * q, 0, 16);
+}
+
+// Check the tags of a run and unpack it into a fragment.
+template <int MMA>
+__device__ __forceinline__ bool xunpack(const Run<MMA>& r, uint32_t tag, Frag<MMA>& f) {
+  bool ok = true;
+  if constexpr (MMA == MMA_BF16) {
+#pragma unroll
+    for (int q = 0; q < 2; ++q)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        uint32_t w = r.q[q][e];
+        ok &= (w >> 16) == tag;
+        f.v[4 * q + e] = __builtin_bit_cast(__bf16, (unsigned short)(w & 0xffffu));
+      }
+  } else {
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        ok &= r.q[q][2 * e + 1] == tag;
+        f.v[2 * q + e] = u2f(r.q[q][2 * e]);
+      }
+  }
+  return ok;
+}
+
+__device__ __forceinline__ uint32_t load_status(const uint32_t* status) {
+  return __hip_atomic_load(status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void raise_status(uint32_t* status, uint32_t code) {
+  atomicMax(status, code);
+}
+
+__device__ __forceinline__ uint32_t xcc_id() {
+  uint32_t v;
+  asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(v));
+  return v & 0xf;
+}
+
+}  // namespace frnn

@@ -1,0 +1,68 @@
+// The launch plan shared by the host launcher and the kernels.
+//
+// A plan fixes, for one (cell, B, T, N, D, dtype, mma) problem:
+//  * the batch slab of a group (16*NB rows) and the number of slabs;
+//  * KS, the waves per workgroup that split the contraction dimension;
+//  * the workgroup -> (group, hidden tile) map that keeps a group on one XCD;
+//  * the sizes and offsets of every caller-owned area.
+// Forward and backward of one problem use the same plan, so the
+// saved-for-backward area can be laid out exactly as the lanes own it.
+#pragma once
+
+#include <stdint.h>
+
+namespace frnn {
+
+constexpr int kXcds = 8;      // MI355X: 8 XCDs, workgroup w is dispatched to XCD w % 8
+constexpr int kMaxKT = 8;     // max 32-wide k-tiles per gate and wave (forward)
+constexpr int kMaxNFB = 32;   // max 32-wide k-tiles per wave (backward)
+
+struct Plan {
+  int cell, B, T, N, D;
+  int GR, GW, GT, S;
+  int mma, dt_io, dt_state, flags;
+  int NB;          // 16-row batch tiles per group
+  int BS;          // slab rows = 16 * NB
+  int nslab;       // ceil(B / BS)
+  int Bp8;         // B rounded up to 8 (dR GEMM chunking)
+  int ngroups;     // N * nslab
+  int wpg;         // workgroups per group = D / (16 * NDT)
+  int KS;          // waves per hidden tile (contraction split)
+  int NDT;         // hidden tiles per workgroup (workgroup = NDT * KS waves)
+  int grid;        // launched workgroups (idle ones exit at once)
+  int nwg;         // active workgroups = ngroups * wpg
+  int kt_fwd;      // D / 32
+  int kt_bwd;      // GR * D / 32
+  int epl;         // owned elements per lane = ceil(4 * NB / KS)
+  int nsave;       // saved floats per owned element and step
+  // byte sizes / offsets
+  long long xwords_fwd, xwords_bwd;   // exchange words per parity
+  long long save_floats;              // lane-native saved values
+  long long hsave_elems;              // bf16 h_{t-1} for the dR GEMM: [N][T][Bp8/8][D][8]
+  long long dgsave_elems;             // bf16 dG for the dR GEMM: [N][T][Bp8/8][GR*D][8]
+  int splitk;                         // dR GEMM split over K
+  long long ws_fwd, ws_bwd, save_bytes;
+  long long off_save_h, off_save_dg;  // in the save area (bytes); lane-native floats start at 0
+  long long off_x, off_flag;          // workspace offsets (status word at 0)
+  long long off_part, off_dbpart;     // backward: dR split-K partials, db partials
+};
+
+// Group / tile of a workgroup; returns false for an idle workgroup.
+#if defined(__HIPCC__)
+__host__ __device__
+#endif
+inline bool wg_decode(const Plan& p, int wg, int* group, int* member) {
+  if (p.flags & 2) {  // placement-free exchange: compact grid
+    *group = wg / p.wpg;
+    *member = wg % p.wpg;
+    return *group < p.ngroups;
+  }
+  const int xcd = wg % kXcds;
+  const int idx = wg / kXcds;
+  const int slot = idx / p.wpg;
+  *member = idx % p.wpg;
+  *group = slot * kXcds + xcd;
+  return *group < p.ngroups;
+}
+
+}  // namespace frnn

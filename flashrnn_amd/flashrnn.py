@@ -1,0 +1,258 @@
+"""Public entry point: ``flashrnn(Wx, R, b, states, function, config, backend, dtype)``.
+
+Drop-in for the reference's ``flashrnn()`` (``flashrnn/flashrnn/flashrnn.py:1117-1138``)
+on its fused backend: same signature, same public layouts, same return value
+``(states [S,B,T,N,D], last [S,B,1,N,D])``, gradients to all four inputs.
+The work runs in ``libfrnn.so`` (hand-written gfx950 HIP kernels) through the
+C ABI of ``include/frnn.h``; PyTorch provides device memory and the stream.
+
+Shapes (``flashrnn.py:46-68``): ``Wx [B,T,G_W,N,D]``, ``R [G_R,N,D,D]`` (output
+index before input index), ``b [G_T,N,D]``, ``states [S,B,1,N,D]``; per cell
+``(G_R, G_W, G_T, S)`` = lstm (4,4,4,2), slstm (4,4,4,4), gru (3,3,4,1),
+elman (1,1,1,1).
+
+Numerics. ``dtype="bfloat16"`` (the default, as in the reference) runs the
+recurrent product with BF16 operands and FP32 accumulation and keeps every
+state and the pointwise cell in FP32: the reference's
+``numerics="fp32_state_bf16_mma"`` policy (``flashrnn2/torch_backend.py:21-35``).
+``dtype="float32"`` runs the product in FP32 (the mathematical policy).
+Inputs may be BF16 or FP32 in either mode; outputs use the dtype of ``Wx``.
+
+``last`` is the full-precision carry: it has the dtype of the ``states``
+argument (FP32 carries in give FP32 carries out), so chunked calls continue
+exactly where the unchunked call would be (``docs/flashrnn2/persistent-continuation.md``).
+"""
+
+from __future__ import annotations
+
+import collections
+import os
+from dataclasses import dataclass
+from typing import Optional
+
+import torch
+import torch.nn.functional as F
+
+from . import _lib
+
+# (G_R, G_W, G_T, S); rnn_function_registry, flashrnn.py:46-68
+CELL_SIZES = {"lstm": (4, 4, 4, 2), "slstm": (4, 4, 4, 4), "gru": (3, 3, 4, 1), "elman": (1, 1, 1, 1)}
+FUSED_BACKENDS = ("cuda_fused", "fused", "hip_fused")
+DTYPES = {"bfloat16": torch.bfloat16, "float32": torch.float32}
+_IO = {torch.float32: _lib.FRNN_F32, torch.bfloat16: _lib.FRNN_BF16}
+
+
+@dataclass
+class FlashRNNConfig:
+    """The subset of the reference's ``FlashRNNConfig`` (``flashrnn.py:121-380``)
+    that applies to the fused path. Options of the reference that this build
+    does not implement yet raise ``NotImplementedError`` instead of being ignored."""
+
+    backend: str = "cuda_fused"
+    function: str = "lstm"
+    dtype: str = "bfloat16"
+    gradient_recurrent_cut: bool = False
+    gradient_recurrent_clipval: Optional[float] = None
+    forward_clipval: Optional[float] = None
+    num_heads: int = -1
+    head_dim: int = -1
+    batch_size: int = -1
+
+    def __post_init__(self):
+        if self.function not in CELL_SIZES:
+            raise ValueError(f"RNN function {self.function} not in registry")
+        if self.backend not in FUSED_BACKENDS:
+            raise ValueError(
+                f"backend {self.backend!r} is not provided by flashrnn_amd; "
+                f"use one of {FUSED_BACKENDS} (the HIP fused recurrence)"
+            )
+        if self.dtype not in DTYPES:
+            raise ValueError(f"dtype {self.dtype!r} not supported; use one of {tuple(DTYPES)}")
+        if self.gradient_recurrent_cut or self.gradient_recurrent_clipval is not None or self.forward_clipval is not None:
+            raise NotImplementedError("gradient cut and clip options are not implemented in flashrnn_amd yet")
+        (self.num_gates_r, self.num_gates_w, self.num_gates_t, self.num_states) = CELL_SIZES[self.function]
+
+
+# ----------------------------------------------------------------- status handling
+_state = {"xcd_shared": os.environ.get("FRNN_XCD_SHARED", "0") == "1",
+          "strict": os.environ.get("FRNN_SYNC_CHECK", "0") == "1"}
+_pending: collections.deque = collections.deque()
+
+
+def set_strict(flag: bool) -> None:
+    """Strict mode: wait for every call and raise on a device-side error at once."""
+    _state["strict"] = bool(flag)
+
+
+def _raise_status(code: int) -> None:
+    if code == _lib.FRNN_E_PLACEMENT:
+        _state["xcd_shared"] = True  # later calls use the placement-free exchange
+    raise RuntimeError(f"flashrnn_amd device error: {_lib.strerror(code)} (code {code})")
+
+
+def _drain_pending(block: bool = False) -> None:
+    while _pending:
+        host, event = _pending[0]
+        if not block and not event.query():
+            return
+        event.synchronize()
+        _pending.popleft()
+        v = int(host[0])
+        if v:
+            _raise_status(-v)
+
+
+def synchronize_and_check() -> None:
+    """Wait for all outstanding calls and raise if any reported a device error."""
+    _drain_pending(block=True)
+
+
+def _after_call(ws: torch.Tensor) -> None:
+    if _state["strict"]:
+        rc = _lib.load().frnn_status(ws.data_ptr(), torch.cuda.current_stream(ws.device).cuda_stream)
+        if rc != _lib.FRNN_OK:
+            _raise_status(rc)
+        return
+    host = torch.empty(1, dtype=torch.int32, pin_memory=True)
+    host.copy_(ws[:4].view(torch.int32), non_blocking=True)
+    ev = torch.cuda.Event()
+    ev.record()
+    _pending.append((host, ev))
+
+
+def _workspace(nbytes: int, device) -> torch.Tensor:
+    ws = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=device)
+    ws[:256].zero_()  # the status word is sticky; it starts clear
+    return ws
+
+
+# --------------------------------------------------------------------- autograd
+def _desc(cell, B, T, N, D, io, st, mma, training):
+    flags = (_lib.FRNN_TRAINING if training else 0) | (_lib.FRNN_XCD_SHARED if _state["xcd_shared"] else 0)
+    return _lib.FrnnDesc(_lib.CELLS[cell], B, T, N, D, _IO[io], _IO[st], mma, flags)
+
+
+class _FusedRecurrence(torch.autograd.Function):
+    """Autograd contract of the reference's FlashRNNFunctionFused
+    (``flashrnn.py:697-802``): saves what the backward kernel needs, returns
+    gradients for Wx, R, b and the initial state."""
+
+    @staticmethod
+    def forward(ctx, wx, R, b, s0, cell, mma):
+        _drain_pending()
+        lib = _lib.load()
+        B, T, _, N, D = wx.shape
+        training = torch.is_grad_enabled() or any(ctx.needs_input_grad[:4])
+        d = _desc(cell, B, T, N, D, wx.dtype, s0.dtype, mma, training)
+        dev = wx.device
+        S = CELL_SIZES[cell][3]
+        states = torch.empty((S, B, T, N, D), dtype=wx.dtype, device=dev)
+        carry = torch.empty((S, B, N, D), dtype=s0.dtype, device=dev)
+        ws = _workspace(lib.frnn_workspace_bytes(d, 0), dev)
+        save = torch.empty(lib.frnn_workspace_bytes(d, 2), dtype=torch.uint8, device=dev) if training else None
+        stream = torch.cuda.current_stream(dev).cuda_stream
+        rc = lib.frnn_fwd(
+            d, wx.data_ptr(), R.data_ptr(), b.data_ptr(), s0.data_ptr(), states.data_ptr(), carry.data_ptr(),
+            save.data_ptr() if save is not None else None, ws.data_ptr(), ws.numel(), stream,
+        )
+        _lib.check(rc, "frnn_fwd")
+        _after_call(ws)
+        if training:
+            ctx.save_for_backward(R, s0, save)
+            ctx.meta = (cell, mma, wx.shape, wx.dtype, b.shape)
+        return states, carry
+
+    @staticmethod
+    def backward(ctx, d_states, d_carry):
+        _drain_pending()
+        lib = _lib.load()
+        R, s0, save = ctx.saved_tensors
+        cell, mma, wshape, io, bshape = ctx.meta
+        B, T, _, N, D = wshape
+        d = _desc(cell, B, T, N, D, io, s0.dtype, mma, True)
+        dev = R.device
+        d_states = d_states.to(io).contiguous() if d_states is not None else None
+        d_carry = d_carry.to(s0.dtype).contiguous() if d_carry is not None else None
+        dwx = torch.empty(wshape, dtype=io, device=dev)
+        dR = torch.empty(R.shape, dtype=io, device=dev)
+        db = torch.empty(bshape, dtype=io, device=dev)
+        ds0 = torch.empty(s0.shape, dtype=s0.dtype, device=dev)
+        ws = _workspace(lib.frnn_workspace_bytes(d, 1), dev)
+        stream = torch.cuda.current_stream(dev).cuda_stream
+        rc = lib.frnn_bwd(
+            d, R.data_ptr(), s0.data_ptr(), save.data_ptr(),
+            d_states.data_ptr() if d_states is not None else None,
+            d_carry.data_ptr() if d_carry is not None else None,
+            dwx.data_ptr(), dR.data_ptr(), db.data_ptr(), ds0.data_ptr(), ws.data_ptr(), ws.numel(), stream,
+        )
+        _lib.check(rc, "frnn_bwd")
+        _after_call(ws)
+        return dwx, dR, db, ds0, None, None
+
+
+# ----------------------------------------------------------------------- public API
+def _check_shapes(cell, Wx, R, b, states):
+    gr, gw, gt, S = CELL_SIZES[cell]
+    if Wx.ndim != 5:
+        raise ValueError("Wx must have layout [B,T,G,N,D]")
+    B, T, G, N, D = Wx.shape
+    if min(B, T, N, D) < 1:
+        raise ValueError("batch, time, heads and width must be positive")
+    if G != gw:
+        raise ValueError(f"Wx has {G} gates, cell {cell} expects {gw}")
+    if tuple(R.shape) != (gr, N, D, D):
+        raise ValueError(f"recurrent weights must have layout [G,N,D,P] = {(gr, N, D, D)}")
+    if tuple(b.shape) != (gt, N, D):
+        raise ValueError(f"bias must have layout [G,N,D] = {(gt, N, D)}")
+    if states is not None and tuple(states.shape) != (S, B, 1, N, D):
+        raise ValueError(f"initial state must have layout [S,B,1,N,D] = {(S, B, 1, N, D)}")
+    if any(t.device != Wx.device for t in (R, b) + (() if states is None else (states,))):
+        raise ValueError("all inputs must be on the same device")
+    if Wx.device.type != "cuda":
+        raise ValueError("flashrnn_amd runs on a ROCm GPU; inputs must be device tensors")
+
+
+def flashrnn(
+    Wx: torch.Tensor,
+    R: torch.Tensor,
+    b: torch.Tensor,
+    states: Optional[torch.Tensor] = None,
+    function: str = "lstm",
+    config: Optional[FlashRNNConfig] = None,
+    backend: str = "cuda_fused",
+    dtype: str = "bfloat16",
+):
+    """Fused multi-head recurrence. Returns ``(states [S,B,T,N,D], last [S,B,1,N,D])``."""
+    if config is None:
+        config = FlashRNNConfig(backend=backend, function=function, dtype=dtype)
+    cell = config.function
+    _check_shapes(cell, Wx, R, b, states)
+    io = Wx.dtype if Wx.dtype in _IO else torch.float32
+    if Wx.dtype not in _IO:
+        raise ValueError(f"Wx dtype {Wx.dtype} not supported; use bfloat16 or float32")
+    mma = _lib.FRNN_MMA_BF16 if config.dtype == "bfloat16" else _lib.FRNN_MMA_F32
+    B, T, _, N, D = Wx.shape
+    S = CELL_SIZES[cell][3]
+    if states is None:
+        s0 = torch.zeros((S, B, N, D), dtype=io, device=Wx.device)
+    else:
+        st_dtype = states.dtype if states.dtype in _IO else io
+        s0 = states.to(st_dtype)[:, :, 0]
+    R = R.to(io)
+    b = b.to(io)
+    # width: the kernels tile hidden units by 32; pad with inert units (zero
+    # weights, inputs and states), which never reach a real unit.
+    Dp = (D + 31) // 32 * 32
+    if Dp > 1024:
+        raise ValueError(f"head width {D} exceeds the supported maximum 1024")
+    if Dp != D:
+        pad = Dp - D
+        Wx = F.pad(Wx, (0, pad))
+        R = F.pad(R, (0, pad, 0, pad))
+        b = F.pad(b, (0, pad))
+        s0 = F.pad(s0, (0, pad))
+    hist, carry = _FusedRecurrence.apply(Wx.contiguous(), R.contiguous(), b.contiguous(), s0.contiguous(), cell, mma)
+    if Dp != D:
+        hist = hist[..., :D]
+        carry = carry[..., :D]
+    return hist, carry.unsqueeze(2)

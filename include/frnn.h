@@ -1,0 +1,129 @@
+/* frnn.h -- C ABI of the MI355X (gfx950) fused recurrent forward/backward library.
+ *
+ * The library (libfrnn.so) implements the fused multi-head recurrence of
+ * FlashRNN: per step g_t = R . h_{t-1} + Wx_t + b, s_t = P(s_{t-1}, g_t), for
+ * the LSTM, GRU, Elman and sLSTM cells, forward and backward, on one GPU.
+ *
+ * It replaces the reference's native boundary, the pybind class
+ * FlashRNNFuncFused (flashrnn/flashrnn/fused/flashrnn.cc:244-535):
+ *   .forward(training, x, s0, R, b)             (flashrnn.cc:257-333) -> frnn_fwd
+ *   .backward(R_t, b, s, g_r, g_i, ds_new)      (flashrnn.cc:335-435) -> frnn_bwd
+ * and its host launchers ForwardPass::Run / BackwardPass::Run
+ * (fused/flashrnn_fused_forward.cu:773-976, fused/flashrnn_fused_backward.cu:769-1087).
+ *
+ * Differences of contract, on purpose:
+ *  - tensors use the public layouts of flashrnn() (flashrnn/flashrnn/flashrnn.py:1117-1138)
+ *    directly, so the caller makes no permuted copies:
+ *      Wx [B,T,G_W,N,D]  R [G_R,N,D(out),D(in)]  b [G_T,N,D]
+ *      s0 [S,B,N,D] (the [S,B,1,N,D] initial state)  states [S,B,T,N,D]
+ *      carry [S,B,N,D] -- the last state in full FP32 (chunk continuation);
+ *  - shapes and dtypes are runtime arguments (no JIT, no per-shape build);
+ *  - the caller owns every buffer (inputs, outputs, the saved-for-backward
+ *    area and the workspace); the library never allocates and never
+ *    synchronises; all work is enqueued on the caller's stream;
+ *  - errors: a negative return for anything detected on the host; a device
+ *    status word (first 4 bytes of the workspace) for anything detected while
+ *    the kernels run (a recurrence-exchange timeout, a workgroup placement
+ *    that breaks the exchange protocol). frnn_status() reads it.
+ *
+ * Thread safety: stateless and reentrant. Calls that overlap in time must use
+ * distinct workspaces.
+ */
+#ifndef FRNN_H
+#define FRNN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ihipStream_t* frnn_stream_t; /* == hipStream_t */
+
+enum frnn_cell { FRNN_LSTM = 0, FRNN_GRU = 1, FRNN_ELMAN = 2, FRNN_SLSTM = 3 };
+enum frnn_dtype { FRNN_F32 = 0, FRNN_BF16 = 1 };
+/* Recurrent-product arithmetic:
+ *  FRNN_MMA_BF16: R and h_{t-1} rounded to BF16, FP32 accumulation, FP32
+ *    state and pointwise -- the reference's numerics="fp32_state_bf16_mma"
+ *    (flashrnn/flashrnn2/torch_backend.py:21-35). Backward rounds the
+ *    recurrent cotangents through BF16 the same way.
+ *  FRNN_MMA_F32: FP32 operands and accumulation -- numerics="mathematical" in FP32. */
+enum frnn_mma { FRNN_MMA_BF16 = 0, FRNN_MMA_F32 = 1 };
+enum frnn_flags {
+  FRNN_TRAINING = 1,       /* frnn_fwd fills the saved-for-backward area */
+  FRNN_XCD_SHARED = 2,     /* exchange through memory-side coherence (slower; any placement) */
+};
+
+typedef struct frnn_desc {
+  int32_t cell;        /* enum frnn_cell */
+  int32_t batch;       /* B */
+  int32_t steps;       /* T */
+  int32_t heads;       /* N */
+  int32_t width;       /* D, multiple of 32, <= 1024 */
+  int32_t dtype_io;    /* dtype of Wx, R, b, states, dWx, dR, db, d_states */
+  int32_t dtype_state; /* dtype of s0, ds0, carry and d_carry */
+  int32_t mma;         /* enum frnn_mma */
+  int32_t flags;       /* enum frnn_flags */
+} frnn_desc;
+
+enum frnn_status {
+  FRNN_OK = 0,
+  FRNN_E_INVALID = -1,     /* null pointer, bad enum, bad shape */
+  FRNN_E_UNSUPPORTED = -2, /* valid but not implemented (e.g. width not a multiple of 32) */
+  FRNN_E_WORKSPACE = -3,   /* workspace smaller than frnn_workspace_bytes() */
+  FRNN_E_LAUNCH = -4,      /* the HIP runtime refused a launch (co-residency, resources) */
+  FRNN_E_TIMEOUT = -5,     /* device: a recurrence exchange did not arrive within the spin limit */
+  FRNN_E_PLACEMENT = -6,   /* device: a workgroup ran on an unexpected XCD */
+};
+
+/* Gate and state counts of a cell: (G_R, G_W, G_T, S); flashrnn.py:46-68. */
+int frnn_cell_sizes(int cell, int32_t* g_r, int32_t* g_w, int32_t* g_t, int32_t* s);
+
+/* Bytes of the caller-owned areas. which: 0 = forward workspace,
+ * 1 = backward workspace, 2 = saved-for-backward area (written by a training
+ * forward, read by the matching backward). Returns 0 for an invalid desc. */
+size_t frnn_workspace_bytes(const frnn_desc* d, int which);
+
+/* Forward. Replaces FlashRNNFuncFused::forward (fused/flashrnn.cc:257-333).
+ * states_out: [S,B,T,N,D] in dtype_io. carry_out: [S,B,N,D] in dtype_state
+ * (may be NULL). save: the saved-for-backward area (may be NULL unless
+ * FRNN_TRAINING). */
+int frnn_fwd(const frnn_desc* d, const void* wx, const void* R, const void* b, const void* s0,
+             void* states_out, void* carry_out, void* save, void* ws, size_t ws_bytes,
+             frnn_stream_t stream);
+
+/* Backward. Replaces FlashRNNFuncFused::backward (fused/flashrnn.cc:335-435).
+ * d_states: [S,B,T,N,D] (dtype_io, may be NULL = zero); d_carry: [S,B,N,D]
+ * (dtype_state, may be NULL = zero). Outputs dwx [B,T,G_W,N,D], dR
+ * [G_R,N,D,D], db [G_T,N,D] (dtype_io) and ds0 [S,B,N,D] (dtype_state) are
+ * overwritten. R, s0 and save must be those of the training forward. */
+int frnn_bwd(const frnn_desc* d, const void* R, const void* s0, const void* save,
+             const void* d_states, const void* d_carry, void* dwx, void* dR, void* db, void* ds0,
+             void* ws, size_t ws_bytes, frnn_stream_t stream);
+
+/* Waits for the stream, then returns the device status word of ws
+ * (FRNN_OK, FRNN_E_TIMEOUT, FRNN_E_PLACEMENT). */
+int frnn_status(const void* ws, frnn_stream_t stream);
+
+/* Static description of an error code. */
+const char* frnn_strerror(int code);
+
+/* Optional kernel timing. When enabled, every persistent forward recurrence,
+ * backward recurrence and dR GEMM (+ its reduction) launch is bracketed by a
+ * pair of HIP events on the caller's stream (events owned by the library).
+ * frnn_timing_read() waits for the recorded events, returns the summed
+ * milliseconds and launch counts per kind -- [0] forward recurrence,
+ * [1] backward recurrence, [2] dR GEMM + reduction -- and clears the record.
+ * Not reentrant: a profiling aid for one thread. */
+void frnn_timing_enable(int on);
+int frnn_timing_read(double* ms3, int32_t* counts3);
+
+/* Test hook: the spin limit of the exchange waits (default 1<<22 polls).
+ * A tiny value forces FRNN_E_TIMEOUT from the host without faulting. */
+void frnn_set_spin_limit(uint32_t polls);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* FRNN_H */

@@ -1,0 +1,113 @@
+"""GPU parity: the HIP fused recurrence against the CPU oracle (restated flashrnn_torch).
+
+Tolerances, metric max|a-e| / max|e| per tensor:
+  * BF16-operand / FP32-state kernel vs numerics="fp32_state_bf16_mma": 1e-2,
+    on all states and on the gradients of Wx, R, b and the initial state;
+  * FP32 kernel vs numerics="mathematical" in FP32: 1e-4.
+The oracle runs on the CPU on the same seeded inputs.
+"""
+
+import pytest
+import torch
+
+from oracle.torch_restatement import flashrnn_torch
+
+pytestmark = pytest.mark.gpu
+
+SIZES = {"lstm": (4, 4, 4, 2), "slstm": (4, 4, 4, 4), "gru": (3, 3, 4, 1), "elman": (1, 1, 1, 1)}
+TOL = {"bfloat16": 1e-2, "float32": 1e-4}
+
+
+def rel(a, e):
+    a, e = a.detach().double().cpu(), e.detach().double().cpu()
+    return ((a - e).abs().max() / e.abs().max().clamp_min(1e-30)).item()
+
+
+def make(cell, B, T, N, D, seed, zero_state=False, slstm_bias=True):
+    g = torch.Generator().manual_seed(seed)
+    gr, gw, gt, S = SIZES[cell]
+    wx = torch.randn(B, T, gw, N, D, generator=g)
+    R = torch.randn(gr, N, D, D, generator=g) / D**0.5
+    b = 0.1 * torch.randn(gt, N, D, generator=g)
+    s0 = torch.zeros(S, B, 1, N, D) if zero_state else 0.5 * torch.randn(S, B, 1, N, D, generator=g)
+    if cell == "slstm":
+        if slstm_bias:
+            b[1] = 3 + 3 * torch.rand(N, D, generator=g)
+        if not zero_state:
+            s0[2] = s0[2].abs() + 1
+    dh = torch.randn(S, B, T, N, D, generator=g)
+    dl = torch.randn(S, B, 1, N, D, generator=g)
+    return (wx, R, b, s0), dh, dl
+
+
+def run_pair(cell, B, T, N, D, dtype, io=torch.float32, seed=0, zero_state=False):
+    from flashrnn_amd import flashrnn, set_strict
+
+    set_strict(True)
+    cpu, dh, dl = make(cell, B, T, N, D, seed, zero_state)
+    # the kernel sees io-typed inputs; the oracle sees exactly those values in FP32
+    cpu = tuple(t.to(io).float() for t in cpu)
+    numerics = "fp32_state_bf16_mma" if dtype == "bfloat16" else "mathematical"
+    leaves = [t.clone().requires_grad_() for t in cpu]
+    eh, el = flashrnn_torch(*leaves, cell=cell, numerics=numerics)
+    eg = torch.autograd.grad((eh * dh).sum() + (el * dl).sum(), leaves)
+
+    gl = [t.to("cuda", io).requires_grad_() for t in cpu]
+    gl[3] = cpu[3].to("cuda").requires_grad_()  # FP32 carry in -> FP32 carry out
+    ah, al = flashrnn(gl[0], gl[1], gl[2], gl[3], function=cell, dtype=dtype)
+    ag = torch.autograd.grad((ah.float() * dh.cuda()).sum() + (al.float() * dl.cuda()).sum(), gl)
+    torch.cuda.synchronize()
+    return (ah, al, *ag), (eh, el, *eg)
+
+
+CASES = [
+    # cell, B, T, N, D
+    ("lstm", 3, 7, 2, 32),
+    ("lstm", 8, 64, 3, 256),
+    ("lstm", 5, 9, 1, 64),
+    ("gru", 3, 7, 2, 64),
+    ("gru", 16, 16, 1, 768),
+    ("elman", 3, 7, 2, 32),
+    ("elman", 16, 16, 1, 768),
+    ("slstm", 3, 7, 2, 64),
+    ("slstm", 16, 32, 4, 192),
+]
+
+
+@pytest.mark.parametrize("dtype", ["bfloat16", "float32"])
+@pytest.mark.parametrize("cell,B,T,N,D", CASES, ids=[f"{c[0]}-B{c[1]}T{c[2]}N{c[3]}D{c[4]}" for c in CASES])
+def test_parity_fp32_io(cell, B, T, N, D, dtype):
+    if dtype == "float32" and D > 512 and cell != "elman":
+        pytest.skip("FP32-operand mode holds R^T and dG fragments for D <= 512 only (register budget); "
+                    "the library returns FRNN_E_UNSUPPORTED, tested in test_gpu_api")
+    print(f"\n[parity] {cell} B{B} T{T} N{N} D{D} {dtype}", flush=True)
+    actual, expected = run_pair(cell, B, T, N, D, dtype, seed=B * 1000 + D)
+    names = ["states", "last", "dWx", "dR", "db", "ds0"]
+    errs = {k: rel(a, e) for k, a, e in zip(names, actual, expected)}
+    print(errs, flush=True)
+    for k, v in errs.items():
+        assert v <= TOL[dtype], (k, v, errs)
+
+
+@pytest.mark.parametrize("cell", ["lstm", "slstm", "gru", "elman"])
+def test_parity_bf16_io(cell):
+    """BF16 tensors in and out; the oracle sees the same BF16 values in FP32."""
+    print(f"\n[parity-bf16io] {cell}", flush=True)
+    actual, expected = run_pair(cell, 4, 16, 2, 64, "bfloat16", io=torch.bfloat16, seed=5)
+    names = ["states", "last", "dWx", "dR", "db", "ds0"]
+    errs = {k: rel(a, e) for k, a, e in zip(names, actual, expected)}
+    print(errs, flush=True)
+    for k, v in errs.items():
+        assert v <= 1e-2, (k, v, errs)
+
+
+def test_slstm_zero_start():
+    actual, expected = run_pair("slstm", 4, 8, 2, 32, "bfloat16", seed=11, zero_state=True)
+    for a, e in zip(actual, expected):
+        assert rel(a, e) <= 1e-2
+
+
+def test_odd_width_is_padded():
+    actual, expected = run_pair("lstm", 2, 5, 2, 20, "float32", seed=3)
+    for a, e in zip(actual, expected):
+        assert rel(a, e) <= 1e-4
