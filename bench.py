@@ -77,6 +77,7 @@ def main(argv=None):
     ap.add_argument("--steps", type=int, default=30)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--phases", action="store_true", help="also report the in-kernel phase profile")
     args = ap.parse_args(argv)
     if args.gpus != 1:
         print(
@@ -158,6 +159,26 @@ def main(argv=None):
             "traffic": None,
         },
     }
+    if args.phases:
+        prof = torch.zeros(256, dtype=torch.int64, device=dev)
+        lib.frnn_set_phase_profile(prof.data_ptr())
+        step()
+        torch.cuda.synchronize()
+        lib.frnn_set_phase_profile(None)
+        v = prof.cpu().tolist()
+        ckeys = ["exchange_wait", "mfma_lds", "barrier", "cell", "polls"]
+        ikeys = ["ring_fill", "load_issue", "barrier", "drain"]
+        out = {}
+        for d, o in (("fwd", 0), ("bwd", 128)):
+            waves = []
+            for w in range(16):
+                row = v[o + 8 * w: o + 8 * w + 8]
+                if row[5] == 0:
+                    continue
+                keys = ikeys if (w % 5) == 4 else ckeys
+                waves.append({k: round(row[i] / row[5], 1) for i, k in enumerate(keys)})
+            out[d] = waves
+        result["phases_cycles_per_step"] = out
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(torch)
     print(json.dumps(result), flush=True)

@@ -48,6 +48,7 @@ EXPORTS = (
     "frnn_set_spin_limit",
     "frnn_timing_enable",
     "frnn_timing_read",
+    "frnn_set_phase_profile",
 )
 
 _lib = None
@@ -73,7 +74,7 @@ def load(path: str | os.PathLike | None = None) -> ctypes.CDLL:
     lib.frnn_workspace_bytes.restype = sz
     lib.frnn_fwd.argtypes = [dp, vp, vp, vp, vp, vp, vp, vp, vp, sz, vp]
     lib.frnn_fwd.restype = i32
-    lib.frnn_bwd.argtypes = [dp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, sz, vp]
+    lib.frnn_bwd.argtypes = [dp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, sz, vp]
     lib.frnn_bwd.restype = i32
     lib.frnn_status.argtypes = [vp, vp]
     lib.frnn_status.restype = i32
@@ -85,6 +86,8 @@ def load(path: str | os.PathLike | None = None) -> ctypes.CDLL:
     lib.frnn_timing_enable.restype = None
     lib.frnn_timing_read.argtypes = [ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_int32)]
     lib.frnn_timing_read.restype = i32
+    lib.frnn_set_phase_profile.argtypes = [vp]
+    lib.frnn_set_phase_profile.restype = None
     if path is None:
         _lib = lib
     return lib

@@ -19,6 +19,7 @@ namespace {
 using frnn::Plan;
 
 std::atomic<uint32_t> g_spin_limit{1u << 22};
+std::atomic<unsigned long long*> g_phase_prof{nullptr};
 
 // ---- optional kernel timing (frnn_timing_enable / frnn_timing_read)
 struct Timing {
@@ -77,10 +78,16 @@ int nsave_of(int cell) {
   return 0;
 }
 
-// Smallest built k-tiles-per-wave class that holds `need`.
-int ktw_class(int need) {
-  for (int c : {1, 2, 4, 6, 8})
-    if (need <= c) return c;
+// Smallest built k-tiles-per-wave class that holds `need` for a workgroup of
+// `ndt` hidden tiles (one-tile workgroups: 1, 2, 4; two-tile: 6, 8).
+int ktw_class(int need, int ndt) {
+  if (ndt == 1) {
+    for (int c : {1, 2, 4})
+      if (need <= c) return c;
+  } else {
+    for (int c : {6, 8})
+      if (need <= c) return c;
+  }
   return 0;
 }
 
@@ -105,23 +112,20 @@ int make_plan(const frnn_desc* d, Plan* p) {
   p->NB = 1;
   p->BS = 16 * p->NB;
   p->nslab = (p->B + p->BS - 1) / p->BS;
-  p->Bp8 = (p->B + 7) / 8 * 8;
   p->ngroups = p->N * p->nslab;
     p->kt_fwd = p->D / 32;
   p->kt_bwd = p->GR * p->D / 32;
   const int KT = p->kt_fwd;
   // hidden tiles per workgroup: a group must fit the 32 CUs of one XCD
   p->NDT = (p->D / 16 <= 32) ? 1 : 2;
-  // contraction split: more waves per tile shorten the per-step MFMA chain;
-  // the workgroup stays at <= 8 waves (256 VGPRs per lane available)
-  const int max_ks = 8 / p->NDT;
-  p->KS = std::min(std::min(4, max_ks), KT);
-  if (p->mma == FRNN_MMA_F32) p->KS = std::min(max_ks, KT);
-  int need = (KT + p->KS - 1) / p->KS;
-  if (!ktw_class(need)) return FRNN_E_UNSUPPORTED;
+  // contraction split: up to 4 compute waves per tile (+1 I/O wave), a power of two
+  p->KS = KT >= 4 ? 4 : (KT >= 2 ? 2 : 1);
+  const int need = (KT + p->KS - 1) / p->KS;
+  if (!ktw_class(need, p->NDT)) return FRNN_E_UNSUPPORTED;
   // registers per lane held by the resident R^T and the dG fragments of the backward
   const int frag_vgprs = p->mma == FRNN_MMA_BF16 ? 4 : 8;
-  if (2 * p->GR * ktw_class(need) * frag_vgprs > 200) return FRNN_E_UNSUPPORTED;
+  const int vgpr_budget = p->NDT == 1 ? 200 : 112;
+  if (2 * p->GR * ktw_class(need, p->NDT) * frag_vgprs > vgpr_budget) return FRNN_E_UNSUPPORTED;
   p->epl = (4 * p->NB + p->KS - 1) / p->KS;
   p->nsave = nsave_of(p->cell);
   p->wpg = p->D / (16 * p->NDT);
@@ -131,25 +135,21 @@ int make_plan(const frnn_desc* d, Plan* p) {
   const long long wsz = p->mma == FRNN_MMA_BF16 ? 4 : 8;
   p->xwords_fwd = (long long)p->ngroups * p->BS * p->D;
   p->xwords_bwd = (long long)p->ngroups * p->BS * p->GR * p->D;
-  p->save_floats = (long long)p->T * p->nwg * p->nsave * p->NDT * p->KS * 64 * p->epl;
-  const long long KC = (long long)p->T * (p->Bp8 / 8);
-  p->hsave_elems = (long long)p->N * KC * p->D * 8;
-  p->dgsave_elems = (long long)p->N * KC * p->GR * p->D * 8;
-  // dR GEMM split: aim for ~4096 waves, at least 8 k-tiles per split
+  p->save_floats = (long long)p->T * p->nwg * p->nsave * p->NDT * 256 * p->NB;
+  // dR GEMM: 32x32 output tiles, split over K = B*T to fill the GPU (~2048 workgroups, >= 4 k-tiles each)
   const long long tiles = (long long)p->N * (p->GR * p->D / 32) * (p->D / 32);
-  const long long ktt = (KC + 3) / 4;
-  long long split = std::max<long long>(1, 4096 / std::max<long long>(1, tiles));
-  split = std::min<long long>(split, std::max<long long>(1, ktt / 8));
+  const long long ktt = ((long long)p->B * p->T + 31) / 32;
+  long long split = std::max<long long>(1, 2048 / std::max<long long>(1, tiles));
+  split = std::min<long long>(split, std::max<long long>(1, ktt / 4));
   p->splitk = (int)std::min<long long>(split, 64);
-  // saved-for-backward area
-  const long long gsz = p->mma == FRNN_MMA_BF16 ? 2 : 4;  // dR-GEMM operand element
-  p->off_save_h = align_up(p->save_floats * 4);
-  p->save_bytes = align_up(p->off_save_h + p->hsave_elems * gsz);
+  // saved-for-backward area: the lane-native values only
+  p->save_bytes = align_up(p->save_floats * 4);
   // workspaces: status word at 0, exchange at 256
   p->off_x = kAlign;
   p->ws_fwd = align_up(p->off_x + 2 * p->xwords_fwd * wsz);
-  p->off_save_dg = align_up(p->off_x + 2 * p->xwords_bwd * wsz);
-  p->off_part = align_up(p->off_save_dg + p->dgsave_elems * gsz);
+  p->off_dcand = align_up(p->off_x + 2 * p->xwords_bwd * wsz);
+  const long long ndcand = p->cell == FRNN_GRU ? (long long)p->B * p->T * p->N * p->D : 0;
+  p->off_part = align_up(p->off_dcand + ndcand * 4);
   p->off_dbpart = align_up(p->off_part + (long long)p->splitk * p->N * p->GR * p->D * p->D * 4);
   p->ws_bwd = align_up(p->off_dbpart + (long long)p->ngroups * p->GT * p->BS * p->D * 4);
   if (2 * p->xwords_bwd * wsz > 0x7fffffffLL) return FRNN_E_UNSUPPORTED;  // buffer-descriptor range
@@ -160,6 +160,17 @@ int launch(const void* fn, int grid, int block, size_t lds, void* arg, hipStream
   void* args[] = {arg};
   if (hipLaunchKernel(fn, dim3(grid), dim3(block), args, lds, stream) != hipSuccess) {
     (void)hipGetLastError();  // do not leave the error to the caller's next HIP call
+    return FRNN_E_LAUNCH;
+  }
+  return FRNN_OK;
+}
+
+// Dynamic LDS beyond the default 64 KiB needs an explicit per-kernel limit.
+int set_lds_limit(const void* fn, size_t lds) {
+  if (lds > 160 * 1024) return FRNN_E_UNSUPPORTED;
+  if (lds <= 64 * 1024) return FRNN_OK;
+  if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess) {
+    (void)hipGetLastError();
     return FRNN_E_LAUNCH;
   }
   return FRNN_OK;
@@ -236,7 +247,8 @@ int frnn_fwd(const frnn_desc* d, const void* wx, const void* R, const void* b, c
   const bool training = (p.flags & FRNN_TRAINING) != 0;
   if (training && !save) return FRNN_E_INVALID;
   if ((long long)ws_bytes < p.ws_fwd) return FRNN_E_WORKSPACE;
-  const void* fn = frnn::recurrence_kernel(p.cell, p.mma, ktw_class((p.kt_fwd + p.KS - 1) / p.KS), true);
+  const void* fn =
+      frnn::recurrence_kernel(p.cell, p.mma, p.KS, ktw_class((p.kt_fwd + p.KS - 1) / p.KS, p.NDT), p.NDT, true);
   if (!fn) return FRNN_E_UNSUPPORTED;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   char* w = static_cast<char*>(ws);
@@ -251,13 +263,14 @@ int frnn_fwd(const frnn_desc* d, const void* wx, const void* R, const void* b, c
   a.states = states_out;
   a.carry = carry_out;
   a.save = training ? static_cast<float*>(save) : nullptr;
-  a.hsave = training ? static_cast<void*>(static_cast<char*>(save) + p.off_save_h) : nullptr;
   a.xbuf = w + p.off_x;
   a.xbytes = xbytes;
   a.status = reinterpret_cast<uint32_t*>(w);
   a.spin_limit = g_spin_limit.load();
-  const size_t lds = (size_t)2 * p.NDT * p.KS * p.NB * p.GR * 256 * sizeof(float);
-  const int block = 64 * p.NDT * p.KS;
+  a.prof = g_phase_prof.load();
+  const size_t lds = (size_t)p.NDT * frnn::recurrence_lds_floats(p.cell, true, p.KS) * sizeof(float);
+  const int block = 64 * p.NDT * (p.KS + 1);
+  if ((rc = set_lds_limit(fn, lds)) != FRNN_OK) return rc;
   if ((rc = check_residency(p, fn, block, lds)) != FRNN_OK) return rc;
   hipEvent_t t0;
   const bool timed = timing_begin(st, &t0);
@@ -266,20 +279,20 @@ int frnn_fwd(const frnn_desc* d, const void* wx, const void* R, const void* b, c
   return rc;
 }
 
-int frnn_bwd(const frnn_desc* d, const void* R, const void* s0, const void* save, const void* d_states,
-             const void* d_carry, void* dwx, void* dR, void* db, void* ds0, void* ws, size_t ws_bytes,
-             frnn_stream_t stream) {
+int frnn_bwd(const frnn_desc* d, const void* R, const void* s0, const void* states, const void* save,
+             const void* d_states, const void* d_carry, void* dwx, void* dR, void* db, void* ds0, void* ws,
+             size_t ws_bytes, frnn_stream_t stream) {
   Plan p;
   int rc = make_plan(d, &p);
   if (rc != FRNN_OK) return rc;
-  (void)s0;
-  if (!R || !save || !dwx || !dR || !db || !ds0 || !ws) return FRNN_E_INVALID;
+  if (!R || !s0 || !states || !save || !dwx || !dR || !db || !ds0 || !ws) return FRNN_E_INVALID;
   if ((long long)ws_bytes < p.ws_bwd) return FRNN_E_WORKSPACE;
-  const void* fn = frnn::recurrence_kernel(p.cell, p.mma, ktw_class((p.kt_fwd + p.KS - 1) / p.KS), false);
+  const void* fn =
+      frnn::recurrence_kernel(p.cell, p.mma, p.KS, ktw_class((p.kt_fwd + p.KS - 1) / p.KS, p.NDT), p.NDT, false);
   if (!fn) return FRNN_E_UNSUPPORTED;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   char* w = static_cast<char*>(ws);
-  const long long xbytes = p.off_save_dg - p.off_x;
+  const long long xbytes = p.off_dcand - p.off_x;
   if ((rc = clear(w + p.off_x, xbytes, st)) != FRNN_OK) return rc;
   frnn::BwdArgs a;
   a.p = p;
@@ -289,14 +302,16 @@ int frnn_bwd(const frnn_desc* d, const void* R, const void* s0, const void* save
   a.d_carry = d_carry;
   a.dwx = dwx;
   a.ds0 = ds0;
-  a.dgsave = static_cast<void*>(w + p.off_save_dg);
+  a.dcand = reinterpret_cast<float*>(w + p.off_dcand);
   a.dbpart = reinterpret_cast<float*>(w + p.off_dbpart);
   a.xbuf = w + p.off_x;
   a.xbytes = xbytes;
   a.status = reinterpret_cast<uint32_t*>(w);
   a.spin_limit = g_spin_limit.load();
-  const size_t lds = (size_t)2 * p.NDT * p.KS * p.NB * 256 * sizeof(float);
-  const int block = 64 * p.NDT * p.KS;
+  a.prof = g_phase_prof.load();
+  const size_t lds = (size_t)p.NDT * frnn::recurrence_lds_floats(p.cell, false, p.KS) * sizeof(float);
+  const int block = 64 * p.NDT * (p.KS + 1);
+  if ((rc = set_lds_limit(fn, lds)) != FRNN_OK) return rc;
   if ((rc = check_residency(p, fn, block, lds)) != FRNN_OK) return rc;
   hipEvent_t t0;
   bool timed = timing_begin(st, &t0);
@@ -306,15 +321,17 @@ int frnn_bwd(const frnn_desc* d, const void* R, const void* s0, const void* save
 
   frnn::GemmArgs g;
   g.p = p;
-  g.dgsave = a.dgsave;
-  g.hsave = static_cast<const void*>(static_cast<const char*>(save) + p.off_save_h);
+  g.dwx = dwx;
+  g.dcand = a.dcand;
+  g.states = states;
+  g.s0 = s0;
   g.part = reinterpret_cast<float*>(w + p.off_part);
   g.dbpart = a.dbpart;
   g.dR = dR;
   g.db = db;
-  const long long waves = (long long)p.N * (p.GR * p.D / 32) * (p.D / 32) * p.splitk;
+  const long long gwg = (long long)p.N * (p.GR * p.D / 32) * (p.D / 32) * p.splitk;
   timed = timing_begin(st, &t0);
-  rc = launch(frnn::gemm_kernel(p.mma), (int)((waves + 3) / 4), 256, 0, &g, st);
+  rc = launch(frnn::gemm_kernel(p.mma), (int)gwg, 64, 0, &g, st);
   const long long nout = (long long)p.N * p.GR * p.D * p.D + (long long)p.GT * p.N * p.D;
   const int rgrid = (int)std::min<long long>(4096, (nout + 255) / 256);
   if (rc == FRNN_OK) rc = launch(frnn::reduce_kernel(), rgrid, 256, 0, &g, st);
@@ -366,6 +383,10 @@ int frnn_timing_read(double* ms3, int32_t* counts3) {
   }
   g_timing.pending.clear();
   return rc;
+}
+
+void frnn_set_phase_profile(void* device_words) {
+  g_phase_prof.store(static_cast<unsigned long long*>(device_words));
 }
 
 void frnn_set_spin_limit(uint32_t polls) { g_spin_limit.store(polls ? polls : 1u); }

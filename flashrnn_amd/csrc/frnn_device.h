@@ -39,11 +39,9 @@ template <> struct CellShape<CELL_SLSTM> { static constexpr int GR = 4, GW = 4, 
 __device__ __forceinline__ uint32_t f2u(float x) { return __builtin_bit_cast(uint32_t, x); }
 __device__ __forceinline__ float u2f(uint32_t x) { return __builtin_bit_cast(float, x); }
 
-// FP32 -> BF16 bits, round to nearest even; NaN stays a (quiet) NaN.
+// FP32 -> BF16 bits, round to nearest even (gfx950 v_cvt_pk_bf16_f32; NaN stays NaN).
 __device__ __forceinline__ uint32_t bf16_bits(float x) {
-  uint32_t u = f2u(x);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x40u;
-  return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+  return (uint32_t)__builtin_bit_cast(unsigned short, (__bf16)x);
 }
 __device__ __forceinline__ float bf16_to_f32(uint32_t bits) { return u2f(bits << 16); }
 __device__ __forceinline__ float round_bf16(float x) { return bf16_to_f32(bf16_bits(x)); }
@@ -56,6 +54,35 @@ __device__ __forceinline__ float ld_val(const void* p, long i, int dt) {
 __device__ __forceinline__ void st_val(void* p, long i, int dt, float v) {
   if (dt == DT_F32) static_cast<float*>(p)[i] = v;
   else static_cast<unsigned short*>(p)[i] = (unsigned short)bf16_bits(v);
+}
+
+// Four consecutive values, raw: loads issue now and convert later (raw4_f32),
+// so an in-flight load is not waited for at its issue point.
+__device__ __forceinline__ u32x4 ld4_raw(const void* p, long i, int dt) {
+  if (dt == DT_F32) return *reinterpret_cast<const u32x4*>(static_cast<const float*>(p) + i);
+  const uint2 u = *reinterpret_cast<const uint2*>(static_cast<const unsigned short*>(p) + i);
+  return u32x4{u.x, u.y, 0u, 0u};
+}
+__device__ __forceinline__ f32x4 raw4_f32(u32x4 r, int dt) {
+  if (dt == DT_F32) return f32x4{u2f(r[0]), u2f(r[1]), u2f(r[2]), u2f(r[3])};
+  return f32x4{u2f(r[0] << 16), u2f(r[0] & 0xffff0000u), u2f(r[1] << 16), u2f(r[1] & 0xffff0000u)};
+}
+
+// Four consecutive values (16-byte aligned in FP32, 8-byte aligned in BF16).
+__device__ __forceinline__ f32x4 ld4(const void* p, long i, int dt) {
+  if (dt == DT_F32) return *reinterpret_cast<const f32x4*>(static_cast<const float*>(p) + i);
+  const uint2 u = *reinterpret_cast<const uint2*>(static_cast<const unsigned short*>(p) + i);
+  return f32x4{u2f(u.x << 16), u2f(u.x & 0xffff0000u), u2f(u.y << 16), u2f(u.y & 0xffff0000u)};
+}
+__device__ __forceinline__ void st4(void* p, long i, int dt, f32x4 v) {
+  if (dt == DT_F32) {
+    *reinterpret_cast<f32x4*>(static_cast<float*>(p) + i) = v;
+  } else {
+    uint2 u;
+    u.x = bf16_bits(v[0]) | (bf16_bits(v[1]) << 16);
+    u.y = bf16_bits(v[2]) | (bf16_bits(v[3]) << 16);
+    *reinterpret_cast<uint2*>(static_cast<unsigned short*>(p) + i) = u;
+  }
 }
 
 // Activations from the hardware exp2 / log2 / reciprocal (v_exp_f32,
@@ -149,9 +176,9 @@ template <> struct Run<MMA_BF16> { u32x4 q[2]; };
 template <> struct Run<MMA_F32> { u32x4 q[4]; };
 
 template <int MMA>
-__device__ __forceinline__ void xload(const Xchg& x, long word, Run<MMA>& r) {
+__device__ __forceinline__ void xload(const Xchg& x, int word, Run<MMA>& r) {
   constexpr int NQ = MMA == MMA_BF16 ? 2 : 4;
-  const int byte = (int)(word * (MMA == MMA_BF16 ? 4 : 8));
+  const int byte = word * (MMA == MMA_BF16 ? 4 : 8);
 #pragma unroll
   for (int q = 0; q < NQ; ++q) r.q[q] = __builtin_amdgcn_raw_buffer_load_b128(x.rsrc, byte + 16 * q, 0, 16);
 }

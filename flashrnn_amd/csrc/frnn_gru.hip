@@ -1,29 +1,38 @@
-// Recurrence kernels of the gru cell: every (operand type, k-tiles per wave) variant.
+// Recurrence kernels of the gru cell: every built (operand type, contraction
+// split, k-tiles per wave, hidden tiles per workgroup) variant. The planner
+// picks KS = min(4, largest power of two <= D/32); one-tile workgroups
+// (widths up to 512) use k-tile classes 1, 2, 4; two-tile workgroups
+// (widths above 512) use classes 6 and 8 with KS = 4.
 #include "frnn_kernels.h"
 #include "frnn_recurrence.h"
 
 namespace frnn {
 
-template <int MMA, int KTW>
+template <int MMA, int KTW, int NDT, int KS>
 static const void* pick(bool fwd) {
-  return fwd ? reinterpret_cast<const void*>(&fwd_kernel<CELL_GRU, MMA, KTW, 1>)
-             : reinterpret_cast<const void*>(&bwd_kernel<CELL_GRU, MMA, KTW, 1>);
+  return fwd ? reinterpret_cast<const void*>(&fwd_kernel<CELL_GRU, MMA, KTW, 1, NDT, KS>)
+             : reinterpret_cast<const void*>(&bwd_kernel<CELL_GRU, MMA, KTW, 1, NDT, KS>);
 }
 
 template <int MMA>
-static const void* by_ktw(int ktw, bool fwd) {
-  switch (ktw) {
-    case 1: return pick<MMA, 1>(fwd);
-    case 2: return pick<MMA, 2>(fwd);
-    case 4: return pick<MMA, 4>(fwd);
-    case 6: return pick<MMA, 6>(fwd);
-    case 8: return pick<MMA, 8>(fwd);
-  }
+static const void* by_shape(int ks, int ktw, int ndt, bool fwd) {
+  if (ndt == 1 && ks == 1 && ktw == 1) return pick<MMA, 1, 1, 1>(fwd);
+  if (ndt == 1 && ks == 2 && ktw == 1) return pick<MMA, 1, 1, 2>(fwd);
+  if (ndt == 1 && ks == 2 && ktw == 2) return pick<MMA, 2, 1, 2>(fwd);
+  if (ndt == 1 && ks == 4 && ktw == 1) return pick<MMA, 1, 1, 4>(fwd);
+  if (ndt == 1 && ks == 4 && ktw == 2) return pick<MMA, 2, 1, 4>(fwd);
+  if (ndt == 1 && ks == 4 && ktw == 4) return pick<MMA, 4, 1, 4>(fwd);
+  if (ndt == 2 && ks == 4 && ktw == 6) return pick<MMA, 6, 2, 4>(fwd);
+  if (ndt == 2 && ks == 4 && ktw == 8) return pick<MMA, 8, 2, 4>(fwd);
   return nullptr;
 }
 
-const void* gru_kernel(int mma, int ktw, bool forward) {
-  return mma == MMA_BF16 ? by_ktw<MMA_BF16>(ktw, forward) : by_ktw<MMA_F32>(ktw, forward);
+const void* gru_kernel(int mma, int ks, int ktw, int ndt, bool forward) {
+  return mma == MMA_BF16 ? by_shape<MMA_BF16>(ks, ktw, ndt, forward) : by_shape<MMA_F32>(ks, ktw, ndt, forward);
+}
+
+long gru_lds_floats(bool forward, int ks) {
+  return forward ? Lds<CELL_GRU, 1>::fwd(ks) : Lds<CELL_GRU, 1>::bwd(ks);
 }
 
 }  // namespace frnn

@@ -16,11 +16,11 @@ struct FwdArgs {
   void* states;
   void* carry;
   float* save;              // lane-native saved values (training) or null
-  void* hsave;              // h_{t-1} copy for the dR GEMM (bf16 or f32 per mma; training) or null
   char* xbuf;               // exchange, both parities
   long long xbytes;
   uint32_t* status;
   uint32_t spin_limit;
+  unsigned long long* prof;  // phase profile (8 words) or null
 };
 
 struct BwdArgs {
@@ -31,18 +31,23 @@ struct BwdArgs {
   const void* d_carry;      // may be null
   void* dwx;
   void* ds0;
-  void* dgsave;             // dG copy for the dR GEMM (bf16 or f32 per mma)
+  float* dcand;             // GRU: cotangent of the R-only candidate gate [B,T,N,D] (dR GEMM operand)
   float* dbpart;
   char* xbuf;
   long long xbytes;
   uint32_t* status;
   uint32_t spin_limit;
+  unsigned long long* prof;  // phase profile (8 words, after the forward's 8) or null
 };
 
+// dR[g,n,o,p] = sum over (b,t) of dG[b,t,g,n,o] h_{t-1}[b,n,p], read from the
+// public dWx (GRU: gate 0 from dcand) and the forward's state output (h_{-1} = s0).
 struct GemmArgs {
   Plan p;
-  const void* dgsave;
-  const void* hsave;
+  const void* dwx;
+  const float* dcand;
+  const void* states;
+  const void* s0;
   float* part;
   const float* dbpart;
   void* dR;
@@ -50,17 +55,32 @@ struct GemmArgs {
 };
 
 // Persistent recurrence kernel for (mma, k-tiles per wave) of one cell; null if not built.
-const void* lstm_kernel(int mma, int ktw, bool forward);
-const void* gru_kernel(int mma, int ktw, bool forward);
-const void* elman_kernel(int mma, int ktw, bool forward);
-const void* slstm_kernel(int mma, int ktw, bool forward);
+const void* lstm_kernel(int mma, int ks, int ktw, int ndt, bool forward);
+const void* gru_kernel(int mma, int ks, int ktw, int ndt, bool forward);
+const void* elman_kernel(int mma, int ks, int ktw, int ndt, bool forward);
+const void* slstm_kernel(int mma, int ks, int ktw, int ndt, bool forward);
+// LDS floats per hidden-tile team of the persistent kernels (KS compute waves).
+long lstm_lds_floats(bool forward, int ks);
+long gru_lds_floats(bool forward, int ks);
+long elman_lds_floats(bool forward, int ks);
+long slstm_lds_floats(bool forward, int ks);
 
-inline const void* recurrence_kernel(int cell, int mma, int ktw, bool forward) {
+inline long recurrence_lds_floats(int cell, bool forward, int ks) {
   switch (cell) {
-    case 0: return lstm_kernel(mma, ktw, forward);
-    case 1: return gru_kernel(mma, ktw, forward);
-    case 2: return elman_kernel(mma, ktw, forward);
-    case 3: return slstm_kernel(mma, ktw, forward);
+    case 0: return lstm_lds_floats(forward, ks);
+    case 1: return gru_lds_floats(forward, ks);
+    case 2: return elman_lds_floats(forward, ks);
+    case 3: return slstm_lds_floats(forward, ks);
+  }
+  return 0;
+}
+
+inline const void* recurrence_kernel(int cell, int mma, int ks, int ktw, int ndt, bool forward) {
+  switch (cell) {
+    case 0: return lstm_kernel(mma, ks, ktw, ndt, forward);
+    case 1: return gru_kernel(mma, ks, ktw, ndt, forward);
+    case 2: return elman_kernel(mma, ks, ktw, ndt, forward);
+    case 3: return slstm_kernel(mma, ks, ktw, ndt, forward);
   }
   return nullptr;
 }

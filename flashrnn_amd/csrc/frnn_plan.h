@@ -24,7 +24,6 @@ struct Plan {
   int NB;          // 16-row batch tiles per group
   int BS;          // slab rows = 16 * NB
   int nslab;       // ceil(B / BS)
-  int Bp8;         // B rounded up to 8 (dR GEMM chunking)
   int ngroups;     // N * nslab
   int wpg;         // workgroups per group = D / (16 * NDT)
   int KS;          // waves per hidden tile (contraction split)
@@ -38,11 +37,9 @@ struct Plan {
   // byte sizes / offsets
   long long xwords_fwd, xwords_bwd;   // exchange words per parity
   long long save_floats;              // lane-native saved values
-  long long hsave_elems;              // bf16 h_{t-1} for the dR GEMM: [N][T][Bp8/8][D][8]
-  long long dgsave_elems;             // bf16 dG for the dR GEMM: [N][T][Bp8/8][GR*D][8]
   int splitk;                         // dR GEMM split over K
   long long ws_fwd, ws_bwd, save_bytes;
-  long long off_save_h, off_save_dg;  // in the save area (bytes); lane-native floats start at 0
+  long long off_dcand;                // backward workspace: GRU candidate-gate cotangents
   long long off_x, off_flag;          // workspace offsets (status word at 0)
   long long off_part, off_dbpart;     // backward: dR split-K partials, db partials
 };

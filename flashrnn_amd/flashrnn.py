@@ -158,7 +158,7 @@ class _FusedRecurrence(torch.autograd.Function):
         _lib.check(rc, "frnn_fwd")
         _after_call(ws)
         if training:
-            ctx.save_for_backward(R, s0, save)
+            ctx.save_for_backward(R, s0, states, save)
             ctx.meta = (cell, mma, wx.shape, wx.dtype, b.shape)
         return states, carry
 
@@ -166,7 +166,7 @@ class _FusedRecurrence(torch.autograd.Function):
     def backward(ctx, d_states, d_carry):
         _drain_pending()
         lib = _lib.load()
-        R, s0, save = ctx.saved_tensors
+        R, s0, states, save = ctx.saved_tensors
         cell, mma, wshape, io, bshape = ctx.meta
         B, T, _, N, D = wshape
         d = _desc(cell, B, T, N, D, io, s0.dtype, mma, True)
@@ -180,7 +180,7 @@ class _FusedRecurrence(torch.autograd.Function):
         ws = _workspace(lib.frnn_workspace_bytes(d, 1), dev)
         stream = torch.cuda.current_stream(dev).cuda_stream
         rc = lib.frnn_bwd(
-            d, R.data_ptr(), s0.data_ptr(), save.data_ptr(),
+            d, R.data_ptr(), s0.data_ptr(), states.data_ptr(), save.data_ptr(),
             d_states.data_ptr() if d_states is not None else None,
             d_carry.data_ptr() if d_carry is not None else None,
             dwx.data_ptr(), dR.data_ptr(), db.data_ptr(), ds0.data_ptr(), ws.data_ptr(), ws.numel(), stream,

@@ -94,11 +94,12 @@ int frnn_fwd(const frnn_desc* d, const void* wx, const void* R, const void* b, c
              frnn_stream_t stream);
 
 /* Backward. Replaces FlashRNNFuncFused::backward (fused/flashrnn.cc:335-435).
- * d_states: [S,B,T,N,D] (dtype_io, may be NULL = zero); d_carry: [S,B,N,D]
- * (dtype_state, may be NULL = zero). Outputs dwx [B,T,G_W,N,D], dR
- * [G_R,N,D,D], db [G_T,N,D] (dtype_io) and ds0 [S,B,N,D] (dtype_state) are
- * overwritten. R, s0 and save must be those of the training forward. */
-int frnn_bwd(const frnn_desc* d, const void* R, const void* s0, const void* save,
+ * R, s0, states (the forward's states_out) and save must be those of the
+ * training forward. d_states: [S,B,T,N,D] (dtype_io, may be NULL = zero);
+ * d_carry: [S,B,N,D] (dtype_state, may be NULL = zero). Outputs dwx
+ * [B,T,G_W,N,D], dR [G_R,N,D,D], db [G_T,N,D] (dtype_io) and ds0 [S,B,N,D]
+ * (dtype_state) are overwritten. */
+int frnn_bwd(const frnn_desc* d, const void* R, const void* s0, const void* states, const void* save,
              const void* d_states, const void* d_carry, void* dwx, void* dR, void* db, void* ds0,
              void* ws, size_t ws_bytes, frnn_stream_t stream);
 
@@ -118,6 +119,15 @@ const char* frnn_strerror(int code);
  * Not reentrant: a profiling aid for one thread. */
 void frnn_timing_enable(int on);
 int frnn_timing_read(double* ms3, int32_t* counts3);
+
+/* Optional phase profile (a profiling aid): when set to a device buffer of
+ * 256 zeroed 64-bit words, every wave of workgroup 0 accumulates cycle counts
+ * of its time loop into 8 words of its own (wave w at 8*w; forward kernel in
+ * words 0-127, backward in 128-255). Compute waves: [0] exchange wait,
+ * [1] MFMA and LDS partials, [2] workgroup barrier, [3] cell arithmetic,
+ * [4] exchange polls, [5] steps. I/O waves: [0] ring fill, [1] load issue,
+ * [2] barrier, [3] output drain, [5] steps. NULL disables. */
+void frnn_set_phase_profile(void* device_words);
 
 /* Test hook: the spin limit of the exchange waits (default 1<<22 polls).
  * A tiny value forces FRNN_E_TIMEOUT from the host without faulting. */

@@ -77,6 +77,9 @@ CASES = [
 @pytest.mark.parametrize("dtype", ["bfloat16", "float32"])
 @pytest.mark.parametrize("cell,B,T,N,D", CASES, ids=[f"{c[0]}-B{c[1]}T{c[2]}N{c[3]}D{c[4]}" for c in CASES])
 def test_parity_fp32_io(cell, B, T, N, D, dtype):
+    if dtype == "bfloat16" and D > 512 and cell in ("gru", "lstm", "slstm"):
+        pytest.skip("two-tile workgroups (D > 512) hold too many R^T/dG fragments for GR >= 3 in the "
+                    "current register plan; the library returns FRNN_E_UNSUPPORTED")
     if dtype == "float32" and D > 512 and cell != "elman":
         pytest.skip("FP32-operand mode holds R^T and dG fragments for D <= 512 only (register budget); "
                     "the library returns FRNN_E_UNSUPPORTED, tested in test_gpu_api")
