@@ -166,7 +166,7 @@ def main(argv=None):
         torch.cuda.synchronize()
         lib.frnn_set_phase_profile(None)
         v = prof.cpu().tolist()
-        ckeys = ["exchange_wait", "mfma_lds", "barrier", "cell", "polls"]
+        ckeys = ["exchange_wait", "mfma_lds", "barrier", "cell", "polls", None, "reduce"]
         ikeys = ["ring_fill", "load_issue", "barrier", "drain"]
         out = {}
         for d, o in (("fwd", 0), ("bwd", 128)):
@@ -175,8 +175,8 @@ def main(argv=None):
                 row = v[o + 8 * w: o + 8 * w + 8]
                 if row[5] == 0:
                     continue
-                keys = ikeys if (w % 5) == 4 else ckeys
-                waves.append({k: round(row[i] / row[5], 1) for i, k in enumerate(keys)})
+                keys = ikeys if row[4] == 0 and row[0] > 0 and w > 0 else ckeys
+                waves.append({k: round(row[i] / row[5], 1) for i, k in enumerate(keys) if k})
             out[d] = waves
         result["phases_cycles_per_step"] = out
     if not args.no_cpu_baseline:

@@ -6,6 +6,7 @@
 
 #include <algorithm>
 #include <atomic>
+#include <cstdlib>
 #include <cstring>
 #include <mutex>
 #include <vector>
@@ -118,14 +119,28 @@ int make_plan(const frnn_desc* d, Plan* p) {
   const int KT = p->kt_fwd;
   // hidden tiles per workgroup: a group must fit the 32 CUs of one XCD
   p->NDT = (p->D / 16 <= 32) ? 1 : 2;
-  // contraction split: up to 4 compute waves per tile (+1 I/O wave), a power of two
+  // contraction split (compute waves per hidden tile, plus one I/O wave): forward
+  // up to 4; backward up to 8 where D/32 >= 8 (its exchange operand is GR times
+  // wider, so splitting it further shortens each wave's poll). FRNN_KS /
+  // FRNN_KS_BWD (environment, read per plan) override within the built set.
   p->KS = KT >= 4 ? 4 : (KT >= 2 ? 2 : 1);
-  const int need = (KT + p->KS - 1) / p->KS;
-  if (!ktw_class(need, p->NDT)) return FRNN_E_UNSUPPORTED;
-  // registers per lane held by the resident R^T and the dG fragments of the backward
-  const int frag_vgprs = p->mma == FRNN_MMA_BF16 ? 4 : 8;
-  const int vgpr_budget = p->NDT == 1 ? 200 : 112;
-  if (2 * p->GR * ktw_class(need, p->NDT) * frag_vgprs > vgpr_budget) return FRNN_E_UNSUPPORTED;
+  p->KSB = (KT >= 8 && p->NDT == 1) ? 8 : p->KS;
+  auto ks_env = [&](const char* name, int* ks) {
+    if (const char* e = std::getenv(name)) {
+      const int v = std::atoi(e);
+      if ((v == 1 || v == 2 || v == 4 || (v == 8 && p->NDT == 1)) && v <= KT) *ks = v;
+    }
+  };
+  ks_env("FRNN_KS", &p->KS);
+  ks_env("FRNN_KS_BWD", &p->KSB);
+  for (int ks : {p->KS, p->KSB}) {
+    const int need = (KT + ks - 1) / ks;
+    if (!ktw_class(need, p->NDT)) return FRNN_E_UNSUPPORTED;
+    // registers per lane held by the resident R^T and the dG fragments of the backward
+    const int frag_vgprs = p->mma == FRNN_MMA_BF16 ? 4 : 8;
+    const int vgpr_budget = p->NDT == 1 ? 200 : 112;
+    if (2 * p->GR * ktw_class(need, p->NDT) * frag_vgprs > vgpr_budget) return FRNN_E_UNSUPPORTED;
+  }
   p->epl = (4 * p->NB + p->KS - 1) / p->KS;
   p->nsave = nsave_of(p->cell);
   p->wpg = p->D / (16 * p->NDT);
@@ -288,7 +303,7 @@ int frnn_bwd(const frnn_desc* d, const void* R, const void* s0, const void* stat
   if (!R || !s0 || !states || !save || !dwx || !dR || !db || !ds0 || !ws) return FRNN_E_INVALID;
   if ((long long)ws_bytes < p.ws_bwd) return FRNN_E_WORKSPACE;
   const void* fn =
-      frnn::recurrence_kernel(p.cell, p.mma, p.KS, ktw_class((p.kt_fwd + p.KS - 1) / p.KS, p.NDT), p.NDT, false);
+      frnn::recurrence_kernel(p.cell, p.mma, p.KSB, ktw_class((p.kt_fwd + p.KSB - 1) / p.KSB, p.NDT), p.NDT, false);
   if (!fn) return FRNN_E_UNSUPPORTED;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   char* w = static_cast<char*>(ws);
@@ -309,8 +324,8 @@ int frnn_bwd(const frnn_desc* d, const void* R, const void* s0, const void* stat
   a.status = reinterpret_cast<uint32_t*>(w);
   a.spin_limit = g_spin_limit.load();
   a.prof = g_phase_prof.load();
-  const size_t lds = (size_t)p.NDT * frnn::recurrence_lds_floats(p.cell, false, p.KS) * sizeof(float);
-  const int block = 64 * p.NDT * (p.KS + 1);
+  const size_t lds = (size_t)p.NDT * frnn::recurrence_lds_floats(p.cell, false, p.KSB) * sizeof(float);
+  const int block = 64 * p.NDT * (p.KSB + 1);
   if ((rc = set_lds_limit(fn, lds)) != FRNN_OK) return rc;
   if ((rc = check_residency(p, fn, block, lds)) != FRNN_OK) return rc;
   hipEvent_t t0;

@@ -135,6 +135,31 @@ __device__ __forceinline__ void frag_set(Frag<MMA_BF16>& f, int j, float x) {
 }
 __device__ __forceinline__ void frag_set(Frag<MMA_F32>& f, int j, float x) { f.v[j] = x; }
 
+// Rotate a fragment by 8 lanes within each 16-lane row (DPP row_ror:8):
+// lane l receives lane l^8's value.
+__device__ __forceinline__ int rot8(int v) { return __builtin_amdgcn_mov_dpp(v, 0x128, 0xf, 0xf, false); }
+__device__ __forceinline__ Frag<MMA_BF16> frag_rot8(const Frag<MMA_BF16>& f) {
+  typedef int i32x4 __attribute__((ext_vector_type(4)));
+  i32x4 v = __builtin_bit_cast(i32x4, f.v);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) v[i] = rot8(v[i]);
+  Frag<MMA_BF16> o;
+  o.v = __builtin_bit_cast(bf16x8, v);
+  return o;
+}
+__device__ __forceinline__ Frag<MMA_F32> frag_rot8(const Frag<MMA_F32>& f) {
+  Frag<MMA_F32> o;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) o.v[i] = __builtin_bit_cast(float, rot8(__builtin_bit_cast(int, f.v[i])));
+  return o;
+}
+template <int MMA>
+__device__ __forceinline__ Frag<MMA> frag_keep(bool keep, const Frag<MMA>& f) {
+  Frag<MMA> z;
+  z.zero();
+  return keep ? f : z;
+}
+
 // ------------------------------------------------------ exchange words
 // BF16 path: 32-bit word = (tag << 16) | bf16 bits.   F32 path: 64-bit word = (tag << 32) | f32 bits.
 // Tags cycle 1,1,2,2,1,1,... so a slot (double-buffered by step parity)
@@ -166,6 +191,28 @@ __device__ __forceinline__ void xstore(const Xchg& x, long word, float v, uint32
     uint64_t* p = reinterpret_cast<uint64_t*>(x.base) + word;
     if (x.shared_xcd) __hip_atomic_store(p, w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     else __builtin_nontemporal_store(w, p);
+  }
+}
+
+// Store the NV exchange words of one element (its gates, contiguous) with one
+// vector store.
+template <int MMA, int NV>
+__device__ __forceinline__ void xstore_vec(const Xchg& x, long word, const float* v, uint32_t tag) {
+  if constexpr (MMA == MMA_BF16) {
+    typedef uint32_t vec_t __attribute__((ext_vector_type(NV)));
+    vec_t w;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) w[i] = (tag << 16) | bf16_bits(v[i]);
+    uint32_t* p = reinterpret_cast<uint32_t*>(x.base) + word;
+    if (x.shared_xcd) {
+#pragma unroll
+      for (int i = 0; i < NV; ++i) __hip_atomic_store(p + i, w[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    } else {
+      __builtin_nontemporal_store(w, reinterpret_cast<vec_t*>(p));
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < NV; ++i) xstore<MMA>(x, word + i, v[i], tag);
   }
 }
 

@@ -1,6 +1,6 @@
 // Recurrence kernels of the lstm cell: every built (operand type, contraction
 // split, k-tiles per wave, hidden tiles per workgroup) variant. The planner
-// picks KS = min(4, largest power of two <= D/32); one-tile workgroups
+// picks KS = min(4, largest power of two <= D/32), or 8 on request; one-tile workgroups
 // (widths up to 512) use k-tile classes 1, 2, 4; two-tile workgroups
 // (widths above 512) use classes 6 and 8 with KS = 4.
 #include "frnn_kernels.h"
@@ -22,6 +22,8 @@ static const void* by_shape(int ks, int ktw, int ndt, bool fwd) {
   if (ndt == 1 && ks == 4 && ktw == 1) return pick<MMA, 1, 1, 4>(fwd);
   if (ndt == 1 && ks == 4 && ktw == 2) return pick<MMA, 2, 1, 4>(fwd);
   if (ndt == 1 && ks == 4 && ktw == 4) return pick<MMA, 4, 1, 4>(fwd);
+  if (ndt == 1 && ks == 8 && ktw == 1) return pick<MMA, 1, 1, 8>(fwd);
+  if (ndt == 1 && ks == 8 && ktw == 2) return pick<MMA, 2, 1, 8>(fwd);
   if (ndt == 2 && ks == 4 && ktw == 6) return pick<MMA, 6, 2, 4>(fwd);
   if (ndt == 2 && ks == 4 && ktw == 8) return pick<MMA, 8, 2, 4>(fwd);
   return nullptr;

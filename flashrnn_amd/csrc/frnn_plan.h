@@ -26,7 +26,8 @@ struct Plan {
   int nslab;       // ceil(B / BS)
   int ngroups;     // N * nslab
   int wpg;         // workgroups per group = D / (16 * NDT)
-  int KS;          // waves per hidden tile (contraction split)
+  int KS;          // forward: compute waves per hidden tile (contraction split)
+  int KSB;         // backward: compute waves per hidden tile
   int NDT;         // hidden tiles per workgroup (workgroup = NDT * KS waves)
   int grid;        // launched workgroups (idle ones exit at once)
   int nwg;         // active workgroups = ngroups * wpg

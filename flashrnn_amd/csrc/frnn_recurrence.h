@@ -37,17 +37,28 @@ struct BwdRing {  // input steps staged ahead, bounded by the I/O wave's registe
   static constexpr int P = 2;
 };
 
+// LDS layout of a team. Everything an owner lane needs for one element is
+// contiguous, so it arrives in a few 16-byte reads issued together:
+//   forward : red  [2][KS][NB][64 lanes][4 regs][4 gates]  MFMA partial sums
+//             xring[P][NE][GWP]                           Wx of the next steps
+//             ost  [2][NE][NOP]                           states + saved values
+//   backward: red  [2][NB][64 lanes][4 regs][KS]          partial R^T dG
+//             iring[P][NE][NOP]                           state cotangents + saved values
+//             ost  [2][NE][4]                             dWx (+ GRU candidate cotangent)
 template <int CELL, int NB>
 struct Lds {
   static constexpr int NE = NB * 256;
   static constexpr int GR = CellShape<CELL>::GR, GW = CellShape<CELL>::GW, S = CellShape<CELL>::S;
   static constexpr int NSAVE = Cell<CELL>::NSAVE;
+  static constexpr int GWP = GW == 1 ? 1 : 4;                // Wx gates per element, padded
+  static constexpr int NOP = (S + NSAVE + 3) / 4 * 4;        // per-element staged values, padded
+  static constexpr int NOB = 4;                              // backward outputs per element, padded
   // floats per team
   __host__ __device__ static constexpr long fwd(int KS) {
-    return 2L * KS * NB * GR * 256 + (long)kFwdRing * GW * NE + 2L * (S + NSAVE) * NE;
+    return 2L * KS * NB * 1024 + (long)kFwdRing * NE * GWP + 2L * NE * NOP;
   }
   __host__ __device__ static constexpr long bwd(int KS) {
-    return 2L * KS * NB * 256 + (long)BwdRing<CELL>::P * (S + NSAVE) * NE + 2L * (GW + (CELL == CELL_GRU ? 1 : 0)) * NE;
+    return 2L * NB * 256 * KS + (long)BwdRing<CELL>::P * NE * NOP + 2L * NE * NOB;
   }
 };
 
@@ -57,7 +68,7 @@ struct Team {
   int group, member, n, slab, dt, wgi;
 };
 
-__device__ __forceinline__ bool team_setup(const Plan& p, Team& tm, uint32_t* status) {
+__device__ __forceinline__ bool team_setup(const Plan& p, Team& tm, uint32_t* status, int KS) {
   if (!wg_decode(p, blockIdx.x, &tm.group, &tm.member)) return false;
   if (!(p.flags & 2) && xcc_id() != (uint32_t)(blockIdx.x % kXcds)) {
     if (threadIdx.x == 0) raise_status(status, ST_PLACEMENT);
@@ -65,8 +76,8 @@ __device__ __forceinline__ bool team_setup(const Plan& p, Team& tm, uint32_t* st
   }
   tm.lane = threadIdx.x & 63;
   tm.w = threadIdx.x >> 6;
-  tm.team = tm.w / (p.KS + 1);
-  tm.kw = tm.w % (p.KS + 1);
+  tm.team = tm.w / (KS + 1);
+  tm.kw = tm.w % (KS + 1);
   tm.row = tm.lane & 15;
   tm.kq = tm.lane >> 4;
   tm.n = tm.group / p.nslab;
@@ -90,8 +101,8 @@ __device__ __forceinline__ Elem elem_of(const Plan& p, const Team& tm, int e) {
   x.real = x.b < p.B;
   return x;
 }
-// Partial-sum position of element e in the MFMA output layout of its batch
-// tile: lane (dd/4)*16 + row, register dd%4 (dd = hidden unit in the tile).
+// Position of element e in the MFMA output layout of its batch tile: lane
+// (dd/4)*16 + row, register dd%4 (dd = hidden unit in the tile), as lane*4 + reg.
 __device__ __forceinline__ int mfma_pos(int e) {
   const int r = e & 255, dd = r & 15, bb = r >> 4;
   return ((dd >> 2) * 16 + bb) * 4 + (dd & 3);
@@ -105,15 +116,16 @@ __device__ __forceinline__ long save_index(const Plan& p, int ne, int t, int wgi
 
 // Phase profile of every wave of workgroup 0 (8 words per wave). Compute
 // waves: cycles in [0] exchange wait, [1] MFMA + LDS partials, [2] barrier,
-// [3] owners' cell work, [4] exchange polls, [5] steps. I/O waves: [0] ring
-// fill (waits for its loads), [1] load issue, [2] barrier, [3] output drain.
+// [3] owners' cell work (backward: pointwise), [4] exchange polls, [5] steps,
+// [6] backward: reduction of the partial cotangents. I/O waves: [0] ring fill
+// (waits for its loads), [1] load issue, [2] barrier, [3] output drain, [5] steps.
 struct Prof {
-  unsigned long long acc[6];
+  unsigned long long acc[8];
   unsigned long long t;
   bool on;
   __device__ __forceinline__ void init(bool enable) {
     on = enable;
-    for (int i = 0; i < 6; ++i) acc[i] = 0;
+    for (int i = 0; i < 8; ++i) acc[i] = 0;
     t = on ? clock64() : 0;
   }
   __device__ __forceinline__ void mark(int k) {
@@ -127,7 +139,7 @@ struct Prof {
   }
   __device__ __forceinline__ void flush(unsigned long long* out) {
     if (on && (threadIdx.x & 63) == 0)
-      for (int i = 0; i < 6; ++i) out[(threadIdx.x >> 6) * 8 + i] = acc[i];
+      for (int i = 0; i < 8; ++i) out[(threadIdx.x >> 6) * 8 + i] = acc[i];
   }
 };
 
@@ -167,6 +179,53 @@ __device__ __forceinline__ uint32_t gather(const Xchg& x, const int (&word)[NB][
   }
 }
 
+// Paired poll for slabs with at most 8 real batch rows (one 16-row tile): the
+// upper half of each 16-lane row (padding columns of the MFMA operand) polls
+// the odd k-tile of each pair for the same batch row, so a lane issues half the
+// loads; the odd tile then moves down 8 lanes (DPP) and the upper lanes are
+// zeroed. word[j] is the run of k-tile j for batch row lane % 8.
+template <int MMA, int NF>
+__device__ __forceinline__ uint32_t gather_pair(const Xchg& x, const int (&word)[NF], bool bv, int off, int nf,
+                                                uint32_t tag, Frag<MMA> (&X)[1][NF], uint32_t* status,
+                                                uint32_t spin_limit, bool& abort) {
+  if (abort) return 0;
+  constexpr int NP = (NF + 1) / 2;
+  const int hi = (threadIdx.x >> 3) & 1;  // lane % 16 >= 8
+  uint32_t spins = 0;
+  while (true) {
+    Run<MMA> r[NP];
+#pragma unroll
+    for (int i = 0; i < NP; ++i)
+      if (2 * i + hi < nf && bv) xload<MMA>(x, word[2 * i + hi] + off, r[i]);
+    bool ok = true;
+    Frag<MMA> f[NP];
+#pragma unroll
+    for (int i = 0; i < NP; ++i) {
+      f[i].zero();
+      if (2 * i + hi < nf && bv) ok &= xunpack<MMA>(r[i], tag, f[i]);
+    }
+    ++spins;
+    if (__all(ok)) {
+#pragma unroll
+      for (int i = 0; i < NP; ++i) {
+        const Frag<MMA> odd = frag_rot8(f[i]);
+        X[0][2 * i] = frag_keep<MMA>(!hi, f[i]);
+        if (2 * i + 1 < NF) X[0][2 * i + 1] = frag_keep<MMA>(!hi, odd);
+      }
+      return spins;
+    }
+    if (spins >= spin_limit) {
+      raise_status(status, ST_TIMEOUT);
+      abort = true;
+      return spins;
+    }
+    if ((spins & 63u) == 0 && load_status(status) != 0) {
+      abort = true;
+      return spins;
+    }
+  }
+}
+
 // ====================================================================== forward
 // I/O lane l serves the elements e = 256*(i/4) + 4*l + i%4: four consecutive
 // hidden units of one batch row, so every global access is one 8/16-byte
@@ -178,7 +237,7 @@ template <int CELL, int MMA, int NB>
 __device__ void fwd_io(const FwdArgs& a, const Team& tm, float* xring, float* ost) {
   using CS = CellShape<CELL>;
   constexpr int GW = CS::GW, S = CS::S, NE = NB * 256, IOQ = NB, P = kFwdRing;  // IOQ quads per lane
-  constexpr int NSAVE = Cell<CELL>::NSAVE, NOUT = S + NSAVE;
+  constexpr int NSAVE = Cell<CELL>::NSAVE, NOP = Lds<CELL, NB>::NOP, GWP = Lds<CELL, NB>::GWP;
   const Plan& p = a.p;
   const int T = p.T, N = p.N, D = p.D, B = p.B;
   const bool training = (p.flags & 1) != 0;
@@ -203,16 +262,21 @@ __device__ void fwd_io(const FwdArgs& a, const Team& tm, float* xring, float* os
 #pragma unroll
     for (int q = 0; q < IOQ; ++q) {
       const int e = e0[q];
+      // the quad's staged vectors, transposed to one f32x4 (4 elements) per value
+      f32x4 in[4][NOP / 4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k)
+#pragma unroll
+        for (int c = 0; c < NOP / 4; ++c) in[k][c] = *reinterpret_cast<const f32x4*>(src + (e + k) * NOP + 4 * c);
+      auto val = [&](int v) { return f32x4{in[0][v / 4][v % 4], in[1][v / 4][v % 4], in[2][v / 4][v % 4], in[3][v / 4][v % 4]}; };
       if (el[q].real)
 #pragma unroll
         for (int k = 0; k < S; ++k)
-          st4(a.states, ((((long)k * B + el[q].b) * T + t) * N + tm.n) * D + el[q].d, p.dt_io,
-              *reinterpret_cast<const f32x4*>(src + k * NE + e));
+          st4(a.states, ((((long)k * B + el[q].b) * T + t) * N + tm.n) * D + el[q].d, p.dt_io, val(k));
       if (training)
 #pragma unroll
         for (int v = 0; v < NSAVE; ++v)
-          *reinterpret_cast<f32x4*>(a.save + save_index(p, NE, t, tm.wgi, v, tm.team, e)) =
-              *reinterpret_cast<const f32x4*>(src + (S + v) * NE + e);
+          *reinterpret_cast<f32x4*>(a.save + save_index(p, NE, t, tm.wgi, v, tm.team, e)) = val(S + v);
     }
   };
 
@@ -228,22 +292,34 @@ __device__ void fwd_io(const FwdArgs& a, const Team& tm, float* xring, float* os
       const int t = t0 + j;
       if (t < T) {
 #pragma unroll
-        for (int q = 0; q < IOQ; ++q)
+        for (int q = 0; q < IOQ; ++q) {
+          f32x4 x[GW];
 #pragma unroll
-          for (int g = 0; g < GW; ++g)
-            *reinterpret_cast<f32x4*>(xring + (j * GW + g) * NE + e0[q]) = raw4_f32(buf[j][q][g], p.dt_io);
+          for (int g = 0; g < GW; ++g) x[g] = raw4_f32(buf[j][q][g], p.dt_io);
+          if constexpr (GWP == 1) {
+            *reinterpret_cast<f32x4*>(xring + (long)j * NE + e0[q]) = x[0];
+          } else {
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+              f32x4 v = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+              for (int g = 0; g < GW; ++g) v[g] = x[g][k];
+              *reinterpret_cast<f32x4*>(xring + ((long)j * NE + e0[q] + k) * GWP) = v;
+            }
+          }
+        }
         prof.mark(0);
         if (t + P < T) load_wx(t + P, buf[j]);
         prof.mark(1);
         __syncthreads();  // step t: Wx_t staged; outputs of step t-1 complete
         prof.mark(2);
-        if (t >= 1) store_out(t - 1, ost + ((t - 1) & 1) * NOUT * NE);
+        if (t >= 1) store_out(t - 1, ost + ((t - 1) & 1) * NOP * NE);
         prof.mark(3);
       }
     }
   }
   __syncthreads();  // outputs of the last step complete
-  store_out(T - 1, ost + ((T - 1) & 1) * NOUT * NE);
+  store_out(T - 1, ost + ((T - 1) & 1) * NOP * NE);
   prof.acc[5] = T;
   prof.flush(a.prof);
 }
@@ -252,17 +328,17 @@ template <int CELL, int MMA, int KTW, int NB, int NDT, int KSC>
 __global__ void __launch_bounds__(64 * (KSC + 1) * NDT) fwd_kernel(FwdArgs a) {
   using CS = CellShape<CELL>;
   constexpr int GR = CS::GR, GW = CS::GW, GT = CS::GT, S = CS::S;
-  constexpr int NE = NB * 256, EPLMAX = 4 * NB / KSC, KS = KSC;
-  constexpr int NSAVE = Cell<CELL>::NSAVE, NOUT = S + NSAVE;
+  constexpr int NE = NB * 256, EPLMAX = (4 * NB + KSC - 1) / KSC, KS = KSC;
+  constexpr int NSAVE = Cell<CELL>::NSAVE, NOP = Lds<CELL, NB>::NOP, GWP = Lds<CELL, NB>::GWP;
   const Plan& p = a.p;
   Team tm;
-  if (!team_setup(p, tm, a.status)) return;
+  if (!team_setup(p, tm, a.status, KSC)) return;
   const int D = p.D, B = p.B, T = p.T, N = p.N;
 
   extern __shared__ float lds[];
-  float* red = lds + tm.team * Lds<CELL, NB>::fwd(KS);  // [2][KS][NB][GR][256]
-  float* xring = red + 2L * KS * NB * GR * 256;         // [P][GW][NE]
-  float* ost = xring + (long)kFwdRing * GW * NE;        // [2][NOUT][NE]
+  float* red = lds + tm.team * Lds<CELL, NB>::fwd(KS);  // [2][KS][NB][64][4][4]
+  float* xring = red + 2L * KS * NB * 1024;             // [P][NE][GWP]
+  float* ost = xring + (long)kFwdRing * NE * GWP;       // [2][NE][NOP]
 
   // sLSTM: the reference's global predicate all(n0 == 0) over the call's whole initial state
   uint32_t zflag = 0;
@@ -312,6 +388,12 @@ __global__ void __launch_bounds__(64 * (KSC + 1) * NDT) fwd_kernel(FwdArgs a) {
     for (int j = 0; j < KTW; ++j) xword[bt][j] = (tm.group * p.BS + bl) * D + (kt0 + j) * 32 + 8 * tm.kq;
   }
   const int xpar = p.ngroups * p.BS * D;  // words per parity
+  // paired-poll runs (slab of <= 8 real rows, see gather_pair)
+  const bool pair = NB == 1 && B <= 8;
+  int xword_pair[KTW];
+#pragma unroll
+  for (int j = 0; j < KTW; ++j) xword_pair[j] = (tm.group * p.BS + (tm.lane & 7)) * D + (kt0 + j) * 32 + 8 * tm.kq;
+  const bool bv_pair = (tm.lane & 7) < B;
 
   // ---- owned elements
   int oe[EPLMAX];
@@ -339,7 +421,10 @@ __global__ void __launch_bounds__(64 * (KSC + 1) * NDT) fwd_kernel(FwdArgs a) {
 
   Prof prof;
   prof.init(a.prof != nullptr && blockIdx.x == 0);
-
+  // Retire every set-up load before the loop: the wait-count pass then sees no
+  // load still pending at the loop head, and does not fence the exchange
+  // stores inside the loop behind one.
+  __builtin_amdgcn_s_waitcnt(0);
   bool abort = false;
   for (int t = 0; t < T; ++t) {
     // ---- 1. h_{t-1} fragments
@@ -355,8 +440,18 @@ __global__ void __launch_bounds__(64 * (KSC + 1) * NDT) fwd_kernel(FwdArgs a) {
             for (int i = 0; i < 8; ++i) frag_set(X[bt][j], i, ld_val(a.s0, base + i, p.dt_state));
           }
     } else {
-      const uint32_t polls = gather<MMA, NB, KTW>(xc, xword, bval, ((t - 1) & 1) * xpar, nkt, step_tag(t - 1), X,
-                                                  a.status, a.spin_limit, abort);
+      uint32_t polls;
+      if constexpr (NB == 1) {
+        if (pair)
+          polls = gather_pair<MMA, KTW>(xc, xword_pair, bv_pair, ((t - 1) & 1) * xpar, nkt, step_tag(t - 1), X,
+                                        a.status, a.spin_limit, abort);
+        else
+          polls = gather<MMA, NB, KTW>(xc, xword, bval, ((t - 1) & 1) * xpar, nkt, step_tag(t - 1), X, a.status,
+                                       a.spin_limit, abort);
+      } else {
+        polls = gather<MMA, NB, KTW>(xc, xword, bval, ((t - 1) & 1) * xpar, nkt, step_tag(t - 1), X, a.status,
+                                     a.spin_limit, abort);
+      }
       prof.add(4, polls);
     }
     prof.mark(0);
@@ -375,35 +470,47 @@ __global__ void __launch_bounds__(64 * (KSC + 1) * NDT) fwd_kernel(FwdArgs a) {
 #pragma unroll
           for (int bt = 0; bt < NB; ++bt) acc[bt][g] = mma(A[g][j], X[bt][j], acc[bt][g]);
       }
-    float* rp = red + (long)(t & 1) * KS * NB * GR * 256;
+    float* rp = red + (long)(t & 1) * KS * NB * 1024;
 #pragma unroll
     for (int bt = 0; bt < NB; ++bt)
 #pragma unroll
-      for (int g = 0; g < GR; ++g)
-        *reinterpret_cast<f32x4*>(rp + (((tm.kw * NB + bt) * GR + g) * 64 + tm.lane) * 4) = acc[bt][g];
+      for (int i = 0; i < 4; ++i) {
+        f32x4 v = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int g = 0; g < GR; ++g) v[g] = acc[bt][g][i];
+        *reinterpret_cast<f32x4*>(rp + (((tm.kw * NB + bt) * 64 + tm.lane) * 4 + i) * 4) = v;
+      }
     prof.mark(1);
     __syncthreads();
     prof.mark(2);
 
     // ---- 3. owners: gates, cell, staged outputs, exchange
-    const float* xr = xring + (long)(t % kFwdRing) * GW * NE;
-    float* os = ost + (long)(t & 1) * NOUT * NE;
+    const float* xr = xring + (long)(t % kFwdRing) * NE * GWP;
+    float* os = ost + (long)(t & 1) * NE * NOP;
 #pragma unroll
     for (int s = 0; s < EPLMAX; ++s) {
       if (!own[s]) continue;
       const int e = oe[s];
-      const int src = (e >> 8) * GR * 256 + mfma_pos(e);
+      const int src = ((e >> 8) * 64 * 4 + mfma_pos(e)) * 4;  // [bt][lane][reg] -> 4 gates
+      f32x4 part[KS];
+#pragma unroll
+      for (int w2 = 0; w2 < KS; ++w2) part[w2] = *reinterpret_cast<const f32x4*>(rp + w2 * NB * 1024 + src);
+      float xcur[GW];
+      if constexpr (GWP == 1) {
+        xcur[0] = xr[e];
+      } else {
+        const f32x4 xv = *reinterpret_cast<const f32x4*>(xr + e * GWP);
+#pragma unroll
+        for (int g = 0; g < GW; ++g) xcur[g] = xv[g];
+      }
       float ry[GR];
 #pragma unroll
       for (int g = 0; g < GR; ++g) {
         float v = 0.f;
-        #pragma unroll
-        for (int w2 = 0; w2 < KS; ++w2) v += rp[w2 * NB * GR * 256 + src + g * 256];
+#pragma unroll
+        for (int w2 = 0; w2 < KS; ++w2) v += part[w2][g];
         ry[g] = v;
       }
-      float xcur[GW];
-#pragma unroll
-      for (int g = 0; g < GW; ++g) xcur[g] = xr[g * NE + e];
       float sv[NSAVE];
       if constexpr (CELL == CELL_GRU) {
         Cell<CELL_GRU>::fwd3(ry, xcur, bias[s], st[s], sv);
@@ -413,12 +520,19 @@ __global__ void __launch_bounds__(64 * (KSC + 1) * NDT) fwd_kernel(FwdArgs a) {
         for (int g = 0; g < GR; ++g) g4[g] = xcur[g] + ry[g] + bias[s][g];
         Cell<CELL>::fwd(g4, st[s], sv, (CELL == CELL_SLSTM && t == 0) ? zflag : 0u);
       }
+      float outv[NOP];
+#pragma unroll
+      for (int k = 0; k < S; ++k) outv[k] = st[s][k];
+#pragma unroll
+      for (int v = 0; v < NSAVE; ++v) outv[S + v] = sv[v];
+#pragma unroll
+      for (int v = S + NSAVE; v < NOP; ++v) outv[v] = 0.f;
+#pragma unroll
+      for (int c = 0; c < NOP / 4; ++c)
+        *reinterpret_cast<f32x4*>(os + e * NOP + 4 * c) = f32x4{outv[4 * c], outv[4 * c + 1], outv[4 * c + 2], outv[4 * c + 3]};
+      // the exchange word goes out last: nothing after it in this step waits for its completion
       if (el[s].real && t + 1 < T)
         xstore<MMA>(xc, (t & 1) * xpar + ((long)tm.group * p.BS + el[s].bl) * D + el[s].d, st[s][0], step_tag(t));
-#pragma unroll
-      for (int k = 0; k < S; ++k) os[k * NE + e] = st[s][k];
-#pragma unroll
-      for (int v = 0; v < NSAVE; ++v) os[(S + v) * NE + e] = sv[v];
     }
     prof.mark(3);
 
@@ -444,8 +558,8 @@ __global__ void __launch_bounds__(64 * (KSC + 1) * NDT) fwd_kernel(FwdArgs a) {
 template <int CELL, int MMA, int NB>
 __device__ void bwd_io(const BwdArgs& a, const Team& tm, float* iring, float* ost) {
   using CS = CellShape<CELL>;
-  constexpr int GR = CS::GR, GW = CS::GW, S = CS::S, NE = NB * 256, IOQ = NB, P = BwdRing<CELL>::P;
-  constexpr int NSAVE = Cell<CELL>::NSAVE, NIN = S + NSAVE, NOUT = GW + (CELL == CELL_GRU ? 1 : 0);
+  constexpr int GW = CS::GW, S = CS::S, NE = NB * 256, IOQ = NB, P = BwdRing<CELL>::P;
+  constexpr int NSAVE = Cell<CELL>::NSAVE, NIN = S + NSAVE, NOP = Lds<CELL, NB>::NOP, NOB = Lds<CELL, NB>::NOB;
   const Plan& p = a.p;
   const int T = p.T, N = p.N, D = p.D, B = p.B;
   const long wx_t = (long)GW * N * D;
@@ -473,11 +587,21 @@ __device__ void bwd_io(const BwdArgs& a, const Team& tm, float* iring, float* os
   auto stage = [&](int slot, const u32x4 (&src)[IOQ][NIN]) {
 #pragma unroll
     for (int q = 0; q < IOQ; ++q) {
+      f32x4 v[NIN];
 #pragma unroll
-      for (int k = 0; k < S; ++k)
-        *reinterpret_cast<f32x4*>(iring + ((long)slot * NIN + k) * NE + e0[q]) = raw4_f32(src[q][k], p.dt_io);
+      for (int k = 0; k < S; ++k) v[k] = raw4_f32(src[q][k], p.dt_io);
 #pragma unroll
-      for (int k = S; k < NIN; ++k) *reinterpret_cast<u32x4*>(iring + ((long)slot * NIN + k) * NE + e0[q]) = src[q][k];
+      for (int k = S; k < NIN; ++k) v[k] = __builtin_bit_cast(f32x4, src[q][k]);
+      // transpose: element e0+m gets its NOP values contiguous
+#pragma unroll
+      for (int m = 0; m < 4; ++m)
+#pragma unroll
+        for (int c = 0; c < NOP / 4; ++c) {
+          f32x4 o;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) o[r] = (4 * c + r < NIN) ? v[4 * c + r < NIN ? 4 * c + r : 0][m] : 0.f;
+          *reinterpret_cast<f32x4*>(iring + ((long)slot * NE + e0[q] + m) * NOP + 4 * c) = o;
+        }
     }
   };
   auto store_out = [&](int it, const float* src) {
@@ -485,16 +609,18 @@ __device__ void bwd_io(const BwdArgs& a, const Team& tm, float* iring, float* os
 #pragma unroll
     for (int q = 0; q < IOQ; ++q) {
       if (!el[q].real) continue;
+      f32x4 in[4];
+#pragma unroll
+      for (int m = 0; m < 4; ++m) in[m] = *reinterpret_cast<const f32x4*>(src + (e0[q] + m) * NOB);
 #pragma unroll
       for (int g = 0; g < GW; ++g)
         st4(a.dwx, ((long)el[q].b * T + t) * wx_t + ((long)g * N + tm.n) * D + el[q].d, p.dt_io,
-            *reinterpret_cast<const f32x4*>(src + g * NE + e0[q]));
+            f32x4{in[0][g], in[1][g], in[2][g], in[3][g]});
       if constexpr (CELL == CELL_GRU)  // the R-only candidate gate's cotangent, for the dR GEMM
         *reinterpret_cast<f32x4*>(a.dcand + (((long)el[q].b * T + t) * N + tm.n) * D + el[q].d) =
-            *reinterpret_cast<const f32x4*>(src + GW * NE + e0[q]);
+            f32x4{in[0][3], in[1][3], in[2][3], in[3][3]};
     }
   };
-  (void)NOUT;
 
   Prof prof;
   prof.init(a.prof != nullptr && blockIdx.x == 0);
@@ -519,7 +645,7 @@ __device__ void bwd_io(const BwdArgs& a, const Team& tm, float* iring, float* os
         }
         __syncthreads();  // iteration it: outputs staged; inputs of it+1 staged
         prof.mark(2);
-        store_out(it, ost + (long)(it & 1) * NOUT * NE);
+        store_out(it, ost + (long)(it & 1) * NOB * NE);
         prof.mark(3);
       }
     }
@@ -532,20 +658,20 @@ template <int CELL, int MMA, int KTW, int NB, int NDT, int KSC>
 __global__ void __launch_bounds__(64 * (KSC + 1) * NDT) bwd_kernel(BwdArgs a) {
   using CS = CellShape<CELL>;
   constexpr int GR = CS::GR, GW = CS::GW, GT = CS::GT, S = CS::S;
-  constexpr int NE = NB * 256, EPLMAX = 4 * NB / KSC, KS = KSC;
-  constexpr int NSAVE = Cell<CELL>::NSAVE, NIN = S + NSAVE, P = BwdRing<CELL>::P;
-  constexpr int NOUT = GW + (CELL == CELL_GRU ? 1 : 0);
+  constexpr int NE = NB * 256, EPLMAX = (4 * NB + KSC - 1) / KSC, KS = KSC;
+  constexpr int NSAVE = Cell<CELL>::NSAVE, P = BwdRing<CELL>::P;
+  constexpr int NOP = Lds<CELL, NB>::NOP, NOB = Lds<CELL, NB>::NOB;
   constexpr int NF = GR * KTW;  // max fragments of R^T per wave
   const Plan& p = a.p;
   Team tm;
-  if (!team_setup(p, tm, a.status)) return;
+  if (!team_setup(p, tm, a.status, KSC)) return;
   const int D = p.D, B = p.B, N = p.N, T = p.T;
   const int GD = GR * D;
 
   extern __shared__ float lds[];
-  float* red = lds + tm.team * Lds<CELL, NB>::bwd(KS);  // [2][KS][NB][256]
-  float* iring = red + 2L * KS * NB * 256;               // [P][NIN][NE]
-  float* ost = iring + (long)P * NIN * NE;               // [2][NOUT][NE]
+  float* red = lds + tm.team * Lds<CELL, NB>::bwd(KS);  // [2][NB][64][4][KS]
+  float* iring = red + 2L * NB * 256 * KS;               // [P][NE][NOP]
+  float* ost = iring + (long)P * NE * NOP;               // [2][NE][NOB]
 
   if (tm.kw == KS) {
     bwd_io<CELL, MMA, NB>(a, tm, iring, ost);
@@ -562,17 +688,18 @@ __global__ void __launch_bounds__(64 * (KSC + 1) * NDT) bwd_kernel(BwdArgs a) {
   const int kt0 = (tm.kw * KT) / KS;
   const int nkt = ((tm.kw + 1) * KT) / KS - kt0;
 
-  // ---- resident R^T: A[j][row = p][k = (g, o)] = R[g, n, o, dt*16 + row]
+  // ---- resident R^T: A[j][row = p][k = (o, g)] = R[g, n, o, dt*16 + row]
   Frag<MMA> A[NF];
 #pragma unroll
   for (int j = 0; j < NF; ++j) {
     A[j].zero();
     if (j < nkt) {
-      const int kk = (kt0 + j) * 32 + 8 * tm.kq;
-      const int g = kk / D, o = kk % D;
+      const int kk = (kt0 + j) * 32 + 8 * tm.kq;  // k = o * GR + g: an element's gates are adjacent
 #pragma unroll
-      for (int i = 0; i < 8; ++i)
-        frag_set(A[j], i, ld_val(a.R, (((long)g * N + tm.n) * D + o + i) * D + tm.dt * 16 + tm.row, p.dt_io));
+      for (int i = 0; i < 8; ++i) {
+        const int g = (kk + i) % GR, o = (kk + i) / GR;
+        frag_set(A[j], i, ld_val(a.R, (((long)g * N + tm.n) * D + o) * D + tm.dt * 16 + tm.row, p.dt_io));
+      }
     }
   }
 
@@ -586,6 +713,11 @@ __global__ void __launch_bounds__(64 * (KSC + 1) * NDT) bwd_kernel(BwdArgs a) {
     for (int j = 0; j < NF; ++j) xword[bt][j] = (tm.group * p.BS + bl) * GD + (kt0 + j) * 32 + 8 * tm.kq;
   }
   const int xpar = p.ngroups * p.BS * GD;
+  const bool pair = NB == 1 && B <= 8;
+  int xword_pair[NF];
+#pragma unroll
+  for (int j = 0; j < NF; ++j) xword_pair[j] = (tm.group * p.BS + (tm.lane & 7)) * GD + (kt0 + j) * 32 + 8 * tm.kq;
+  const bool bv_pair = (tm.lane & 7) < B;
 
   int oe[EPLMAX];
   bool own[EPLMAX];
@@ -615,24 +747,32 @@ __global__ void __launch_bounds__(64 * (KSC + 1) * NDT) bwd_kernel(BwdArgs a) {
 
   Prof prof;
   prof.init(a.prof != nullptr && blockIdx.x == 0);
+  __builtin_amdgcn_s_waitcnt(0);  // no set-up load pending at the loop head (see the forward kernel)
   __syncthreads();  // iteration 0's inputs staged by the I/O wave
   bool abort = false;
   for (int it = 0; it < T; ++it) {
     const int xoff = (it & 1) * xpar;
     // ---- 1. owners: pointwise backward of step t = T-1-it, publish dG_t
-    const float* ir = iring + (long)(it % P) * NIN * NE;
-    float* os = ost + (long)(it & 1) * NOUT * NE;
+    const float* ir = iring + (long)(it % P) * NE * NOP;
+    float* os = ost + (long)(it & 1) * NE * NOB;
 #pragma unroll
     for (int s = 0; s < EPLMAX; ++s) {
       if (!own[s]) continue;
       const int e = oe[s];
+      float in[NOP];
+#pragma unroll
+      for (int c = 0; c < NOP / 4; ++c) {
+        const f32x4 v = *reinterpret_cast<const f32x4*>(ir + e * NOP + 4 * c);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) in[4 * c + r] = v[r];
+      }
       float ds[S];
 #pragma unroll
-      for (int k = 0; k < S; ++k) ds[k] = carry[s][k] + ir[k * NE + e];
+      for (int k = 0; k < S; ++k) ds[k] = carry[s][k] + in[k];
       ds[0] += dhrec[s];
       float sv[NSAVE];
 #pragma unroll
-      for (int v = 0; v < NSAVE; ++v) sv[v] = ir[(S + v) * NE + e];
+      for (int v = 0; v < NSAVE; ++v) sv[v] = in[S + v];
       float dry[GR], dwx[GW], db[GT], cr[S];
       Cell<CELL>::bwd(ds, sv, dry, dwx, db, cr);
       if (!el[s].real) {
@@ -645,21 +785,30 @@ __global__ void __launch_bounds__(64 * (KSC + 1) * NDT) bwd_kernel(BwdArgs a) {
       } else {
 #pragma unroll
         for (int g = 0; g < GT; ++g) dbacc[s][g] += db[g];
-#pragma unroll
-        for (int g = 0; g < GR; ++g)
-          xstore<MMA>(xc, xoff + ((long)tm.group * p.BS + el[s].bl) * GD + g * D + el[s].d, dry[g], step_tag(it));
       }
 #pragma unroll
       for (int k = 0; k < S; ++k) carry[s][k] = cr[k];
+      f32x4 ov = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int g = 0; g < GW; ++g) os[g * NE + e] = dwx[g];
-      if constexpr (CELL == CELL_GRU) os[GW * NE + e] = dry[0];
+      for (int g = 0; g < GW; ++g) ov[g] = dwx[g];
+      if constexpr (CELL == CELL_GRU) ov[3] = dry[0];
+      *reinterpret_cast<f32x4*>(os + e * NOB) = ov;
+      // the element's gate cotangents go out last, as one vector store (layout [b][o][g])
+      if (el[s].real)
+        xstore_vec<MMA, GR>(xc, xoff + (((long)tm.group * p.BS + el[s].bl) * D + el[s].d) * GR, dry, step_tag(it));
     }
     prof.mark(3);
 
     // ---- 2. dh_{t-1} partial = R^T dG_t over this wave's k-tiles
-    const uint32_t polls = gather<MMA, NB, NF>(xc, xword, bval, xoff, nkt, step_tag(it), X, a.status,
-                                               a.spin_limit, abort);
+    uint32_t polls;
+    if constexpr (NB == 1) {
+      if (pair)
+        polls = gather_pair<MMA, NF>(xc, xword_pair, bv_pair, xoff, nkt, step_tag(it), X, a.status, a.spin_limit, abort);
+      else
+        polls = gather<MMA, NB, NF>(xc, xword, bval, xoff, nkt, step_tag(it), X, a.status, a.spin_limit, abort);
+    } else {
+      polls = gather<MMA, NB, NF>(xc, xword, bval, xoff, nkt, step_tag(it), X, a.status, a.spin_limit, abort);
+    }
     prof.add(4, polls);
     prof.mark(0);
     f32x4 acc[NB];
@@ -671,9 +820,11 @@ __global__ void __launch_bounds__(64 * (KSC + 1) * NDT) bwd_kernel(BwdArgs a) {
 #pragma unroll
         for (int bt = 0; bt < NB; ++bt) acc[bt] = mma(A[j], X[bt][j], acc[bt]);
       }
-    float* rp = red + (long)(it & 1) * KS * NB * 256;
+    float* rp = red + (long)(it & 1) * NB * 256 * KS;
 #pragma unroll
-    for (int bt = 0; bt < NB; ++bt) *reinterpret_cast<f32x4*>(rp + ((tm.kw * NB + bt) * 64 + tm.lane) * 4) = acc[bt];
+    for (int bt = 0; bt < NB; ++bt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) rp[((bt * 64 + tm.lane) * 4 + i) * KS + tm.kw] = acc[bt][i];
     prof.mark(1);
     __syncthreads();
     prof.mark(2);
@@ -682,14 +833,26 @@ __global__ void __launch_bounds__(64 * (KSC + 1) * NDT) bwd_kernel(BwdArgs a) {
 #pragma unroll
     for (int s = 0; s < EPLMAX; ++s) {
       if (!own[s]) continue;
-      const int src = (oe[s] >> 8) * 256 + mfma_pos(oe[s]);
+      const int src = ((oe[s] >> 8) * 256 + mfma_pos(oe[s])) * KS;
+      float part[KS];
+      if constexpr (KS % 4 == 0) {
+#pragma unroll
+        for (int c = 0; c < KS / 4; ++c) {
+          const f32x4 v4 = *reinterpret_cast<const f32x4*>(rp + src + 4 * c);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) part[4 * c + r] = v4[r];
+        }
+      } else {
+#pragma unroll
+        for (int w2 = 0; w2 < KS; ++w2) part[w2] = rp[src + w2];
+      }
       float v = 0.f;
-      #pragma unroll
-      for (int w2 = 0; w2 < KS; ++w2) v += rp[w2 * NB * 256 + src];
+#pragma unroll
+      for (int w2 = 0; w2 < KS; ++w2) v += part[w2];
       // the BF16 policy rounds the cotangent of the rounded hidden operand
       dhrec[s] = el[s].real ? (MMA == MMA_BF16 ? round_bf16(v) : v) : 0.f;
     }
-    prof.mark(3);
+    prof.mark(6);
   }
 
   // ---- d(initial state), d(bias) partials

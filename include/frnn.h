@@ -125,8 +125,9 @@ int frnn_timing_read(double* ms3, int32_t* counts3);
  * of its time loop into 8 words of its own (wave w at 8*w; forward kernel in
  * words 0-127, backward in 128-255). Compute waves: [0] exchange wait,
  * [1] MFMA and LDS partials, [2] workgroup barrier, [3] cell arithmetic,
- * [4] exchange polls, [5] steps. I/O waves: [0] ring fill, [1] load issue,
- * [2] barrier, [3] output drain, [5] steps. NULL disables. */
+ * [4] exchange polls, [5] steps, [6] backward partial-sum reduction. I/O
+ * waves: [0] ring fill, [1] load issue, [2] barrier, [3] output drain,
+ * [5] steps. NULL disables. */
 void frnn_set_phase_profile(void* device_words);
 
 /* Test hook: the spin limit of the exchange waits (default 1<<22 polls).
