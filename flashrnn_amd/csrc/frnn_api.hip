@@ -151,11 +151,13 @@ int make_plan(const frnn_desc* d, Plan* p) {
   p->xwords_fwd = (long long)p->ngroups * p->BS * p->D;
   p->xwords_bwd = (long long)p->ngroups * p->BS * p->GR * p->D;
   p->save_floats = (long long)p->T * p->nwg * p->nsave * p->NDT * 256 * p->NB;
-  // dR GEMM: 32x32 output tiles, split over K = B*T to fill the GPU (~2048 workgroups, >= 4 k-tiles each)
-  const long long tiles = (long long)p->N * (p->GR * p->D / 32) * (p->D / 32);
+  // dR GEMM: 64x64 workgroup tiles where D % 64 == 0 (else 32x32), split over
+  // K = B*T to fill the GPU (~1024 workgroups, >= 8 k-steps of 32 each)
+  const int tile = p->D % 64 == 0 ? 64 : 32;
+  const long long tiles = (long long)p->N * (p->GR * p->D / tile) * (p->D / tile);
   const long long ktt = ((long long)p->B * p->T + 31) / 32;
-  long long split = std::max<long long>(1, 2048 / std::max<long long>(1, tiles));
-  split = std::min<long long>(split, std::max<long long>(1, ktt / 4));
+  long long split = std::max<long long>(1, 1024 / std::max<long long>(1, tiles));
+  split = std::min<long long>(split, std::max<long long>(1, ktt / 8));
   p->splitk = (int)std::min<long long>(split, 64);
   // saved-for-backward area: the lane-native values only
   p->save_bytes = align_up(p->save_floats * 4);
@@ -344,9 +346,11 @@ int frnn_bwd(const frnn_desc* d, const void* R, const void* s0, const void* stat
   g.dbpart = a.dbpart;
   g.dR = dR;
   g.db = db;
-  const long long gwg = (long long)p.N * (p.GR * p.D / 32) * (p.D / 32) * p.splitk;
+  const bool wide = p.D % 64 == 0;
+  const int tile = wide ? 64 : 32;
+  const long long gwg = (long long)p.N * (p.GR * p.D / tile) * (p.D / tile) * p.splitk;
   timed = timing_begin(st, &t0);
-  rc = launch(frnn::gemm_kernel(p.mma), (int)gwg, 64, 0, &g, st);
+  rc = launch(frnn::gemm_kernel(p.mma, wide), (int)gwg, wide ? 256 : 64, 0, &g, st);
   const long long nout = (long long)p.N * p.GR * p.D * p.D + (long long)p.GT * p.N * p.D;
   const int rgrid = (int)std::min<long long>(4096, (nout + 255) / 256);
   if (rc == FRNN_OK) rc = launch(frnn::reduce_kernel(), rgrid, 256, 0, &g, st);

@@ -120,12 +120,22 @@ template <> struct Frag<MMA_F32> {
   }
 };
 
+// The B operand passes through an empty asm so the optimizer cannot see that
+// it is zero in some lanes: the MFMA mixes lanes, yet a "zero operand gives C"
+// fold applied per lane would otherwise let the product be skipped or moved
+// into code that runs with only part of the wave active.
 __device__ __forceinline__ f32x4 mma(const Frag<MMA_BF16>& a, const Frag<MMA_BF16>& b, f32x4 c) {
-  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.v, b.v, c, 0, 0, 0);
+  bf16x8 bv = b.v;
+  asm("" : "+v"(bv));
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.v, bv, c, 0, 0, 0);
 }
 __device__ __forceinline__ f32x4 mma(const Frag<MMA_F32>& a, const Frag<MMA_F32>& b, f32x4 c) {
 #pragma unroll
-  for (int i = 0; i < 8; ++i) c = __builtin_amdgcn_mfma_f32_16x16x4f32(a.v[i], b.v[i], c, 0, 0, 0);
+  for (int i = 0; i < 8; ++i) {
+    float bv = b.v[i];
+    asm("" : "+v"(bv));
+    c = __builtin_amdgcn_mfma_f32_16x16x4f32(a.v[i], bv, c, 0, 0, 0);
+  }
   return c;
 }
 
@@ -219,8 +229,14 @@ __device__ __forceinline__ void xstore_vec(const Xchg& x, long word, const float
 // Issue the loads of one 8-word run (8 consecutive k) at word index `word`.
 // sc1 (aux 16) makes the load miss the CU-local L1 and read the L2.
 template <int MMA> struct Run;
-template <> struct Run<MMA_BF16> { u32x4 q[2]; };
-template <> struct Run<MMA_F32> { u32x4 q[4]; };
+template <> struct Run<MMA_BF16> {
+  u32x4 q[2];
+  __device__ __forceinline__ void zero() { q[0] = q[1] = u32x4{0u, 0u, 0u, 0u}; }
+};
+template <> struct Run<MMA_F32> {
+  u32x4 q[4];
+  __device__ __forceinline__ void zero() { q[0] = q[1] = q[2] = q[3] = u32x4{0u, 0u, 0u, 0u}; }
+};
 
 template <int MMA>
 __device__ __forceinline__ void xload(const Xchg& x, int word, Run<MMA>& r) {

@@ -42,94 +42,136 @@ __device__ __forceinline__ void gemm_frag(const typename GemmElem<MMA>::type* ro
   }
 }
 
-template <int MMA>
-__global__ void __launch_bounds__(64) dr_gemm_kernel(GemmArgs a) {
+// Operand runs of 8 contiguous columns for k = (b, t): dG (m = g*D + o) and h_{t-1} (q).
+struct GemmSrc {
+  const GemmArgs* a;
+  int n;
+  __device__ __forceinline__ void load(long k, int m, int q, f32x4 (&va)[2], f32x4 (&vh)[2]) const {
+    const Plan& p = a->p;
+    const long K = (long)p.B * p.T;
+    va[0] = va[1] = vh[0] = vh[1] = f32x4{0.f, 0.f, 0.f, 0.f};
+    if (k >= K) return;
+    const long b = k / p.T, t = k % p.T;
+    const int g = m / p.D, o = m % p.D;
+    if (p.cell == CELL_GRU && g == 0) {
+      const float* src = a->dcand + ((b * p.T + t) * p.N + n) * p.D + o;
+      va[0] = *reinterpret_cast<const f32x4*>(src);
+      va[1] = *reinterpret_cast<const f32x4*>(src + 4);
+    } else {
+      const int gw = p.cell == CELL_GRU ? g - 1 : g;
+      const long i = (b * p.T + t) * p.GW * p.N * p.D + ((long)gw * p.N + n) * p.D + o;
+      va[0] = ld4(a->dwx, i, p.dt_io);
+      va[1] = ld4(a->dwx, i + 4, p.dt_io);
+    }
+    if (t == 0) {
+      const long i = (b * p.N + n) * p.D + q;  // h_{-1} = s0[0]
+      vh[0] = ld4(a->s0, i, p.dt_state);
+      vh[1] = ld4(a->s0, i + 4, p.dt_state);
+    } else {
+      const long i = ((b * p.T + t - 1) * p.N + n) * p.D + q;  // h_{t-1} = states[0][b][t-1]
+      vh[0] = ld4(a->states, i, p.dt_io);
+      vh[1] = ld4(a->states, i + 4, p.dt_io);
+    }
+  }
+};
+
+// Workgroup tile (32*WM) x (32*WQ) of part[split][n][m][q], WM*WQ waves of 32x32
+// each; k in steps of 32 through double-buffered LDS, the next step's global
+// loads in flight while the current step runs on MFMA. Operands are written to
+// LDS transposed ([column][k]) so each MFMA fragment is one 16-byte (bf16) or
+// two 16-byte (f32) reads of 8 consecutive k.
+template <int MMA, int WM, int WQ>
+__global__ void __launch_bounds__(64 * WM * WQ) dr_gemm_kernel(GemmArgs a) {
   typedef typename GemmElem<MMA>::type E;
-  constexpr int LD = 40;  // LDS row stride (32 k + pad), elements
-  __shared__ __attribute__((aligned(16))) E As[32 * LD];
-  __shared__ __attribute__((aligned(16))) E Hs[32 * LD];
+  constexpr int LD = 40;                 // LDS row stride (32 k + pad), elements
+  constexpr int NT = 64 * WM * WQ;       // threads
+  constexpr int RA = 32 * WM * 4 / NT;   // runs of 8 per thread per step: A (32 k x 32*WM m / 8)
+  constexpr int RH = 32 * WQ * 4 / NT;   // and h
+  __shared__ __attribute__((aligned(16))) E As[2][32 * WM * LD];
+  __shared__ __attribute__((aligned(16))) E Hs[2][32 * WQ * LD];
   const Plan& p = a.p;
-  const int lane = threadIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int GD = p.GR * p.D;
-  const int mt = GD / 32, qt = p.D / 32;
+  const int mt = GD / (32 * WM), qt = p.D / (32 * WQ);
   const int tiles = p.N * mt * qt;
   const int split = blockIdx.x / tiles;
   int rem = blockIdx.x % tiles;
   const int n = rem / (mt * qt);
   rem %= mt * qt;
-  const int m0 = (rem / qt) * 32, q0 = (rem % qt) * 32;
-  const int B = p.B, T = p.T, N = p.N, D = p.D;
-  const long K = (long)B * T;
+  const int m0 = (rem / qt) * 32 * WM, q0 = (rem % qt) * 32 * WQ;
+  const long K = (long)p.B * p.T;
   const long KT = (K + 31) / 32;
-  const long k_lo = 32 * (KT * split / p.splitk), k_hi = 32 * (KT * (split + 1) / p.splitk);
-  const long wx_t = (long)p.GW * N * D;
+  const long s_lo = KT * split / p.splitk, s_hi = KT * (split + 1) / p.splitk;
   const int row = lane & 15, kq = lane >> 4;
+  const int wm = w % WM, wq = w / WM;
+  GemmSrc src{&a, n};
+
   f32x4 acc[2][2];
 #pragma unroll
   for (int i = 0; i < 2; ++i)
 #pragma unroll
     for (int j = 0; j < 2; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  for (long k0 = k_lo; k0 < k_hi; k0 += 32) {
-    // 32 k x 32 columns per operand = 128 runs of 8; two per lane and operand
+  // per-thread runs: A run c -> (k = c / (4*WM), column 8*(c % (4*WM))), h likewise with WQ
+  f32x4 ra[RA][2], rh[RH][2];
+  auto fetch = [&](long s) {
 #pragma unroll
-    for (int r = 0; r < 2; ++r) {
-      const int c = lane + 64 * r;
-      const int kl = c >> 2, col = (c & 3) * 8;
-      const long k = k0 + kl;
-      f32x4 va0 = {0.f, 0.f, 0.f, 0.f}, va1 = va0, vh0 = va0, vh1 = va0;
-      if (k < K) {
-        const long b = k / T, t = k % T;
-        const int m = m0 + col, g = m / D, o = m % D;
-        if (p.cell == CELL_GRU && g == 0) {
-          const float* src = a.dcand + ((b * T + t) * N + n) * D + o;
-          va0 = *reinterpret_cast<const f32x4*>(src);
-          va1 = *reinterpret_cast<const f32x4*>(src + 4);
-        } else {
-          const int gw = p.cell == CELL_GRU ? g - 1 : g;
-          const long i = (b * T + t) * wx_t + ((long)gw * N + n) * D + o;
-          va0 = ld4(a.dwx, i, p.dt_io);
-          va1 = ld4(a.dwx, i + 4, p.dt_io);
-        }
-        const int q = q0 + col;
-        if (t == 0) {
-          const long i = (b * N + n) * D + q;  // h_{-1} = s0[0]
-          vh0 = ld4(a.s0, i, p.dt_state);
-          vh1 = ld4(a.s0, i + 4, p.dt_state);
-        } else {
-          const long i = ((b * T + t - 1) * N + n) * D + q;  // h_{t-1} = states[0][b][t-1]
-          vh0 = ld4(a.states, i, p.dt_io);
-          vh1 = ld4(a.states, i + 4, p.dt_io);
-        }
-      }
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        As[(col + i) * LD + kl] = gemm_cvt<MMA>(va0[i]);
-        As[(col + 4 + i) * LD + kl] = gemm_cvt<MMA>(va1[i]);
-        Hs[(col + i) * LD + kl] = gemm_cvt<MMA>(vh0[i]);
-        Hs[(col + 4 + i) * LD + kl] = gemm_cvt<MMA>(vh1[i]);
-      }
+    for (int r = 0; r < RA; ++r) {
+      const int c = tid + NT * r;
+      f32x4 dummy[2];
+      src.load(32 * s + c / (4 * WM), m0 + 8 * (c % (4 * WM)), q0, ra[r], dummy);
     }
+#pragma unroll
+    for (int r = 0; r < RH; ++r) {
+      const int c = tid + NT * r;
+      f32x4 dummy[2];
+      src.load(32 * s + c / (4 * WQ), m0, q0 + 8 * (c % (4 * WQ)), dummy, rh[r]);
+    }
+  };
+  auto stage = [&](int buf) {
+#pragma unroll
+    for (int r = 0; r < RA; ++r) {
+      const int c = tid + NT * r, kl = c / (4 * WM), col = 8 * (c % (4 * WM));
+#pragma unroll
+      for (int i = 0; i < 8; ++i) As[buf][(col + i) * LD + kl] = gemm_cvt<MMA>(ra[r][i / 4][i % 4]);
+    }
+#pragma unroll
+    for (int r = 0; r < RH; ++r) {
+      const int c = tid + NT * r, kl = c / (4 * WQ), col = 8 * (c % (4 * WQ));
+#pragma unroll
+      for (int i = 0; i < 8; ++i) Hs[buf][(col + i) * LD + kl] = gemm_cvt<MMA>(rh[r][i / 4][i % 4]);
+    }
+  };
+
+  if (s_lo < s_hi) {
+    fetch(s_lo);
+    stage(0);
     __syncthreads();
+  }
+  for (long s = s_lo; s < s_hi; ++s) {
+    const int buf = (int)((s - s_lo) & 1);
+    if (s + 1 < s_hi) fetch(s + 1);
     Frag<MMA> fa[2], fh[2];
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
-      gemm_frag<MMA>(As + (i * 16 + row) * LD + 8 * kq, fa[i]);
-      gemm_frag<MMA>(Hs + (i * 16 + row) * LD + 8 * kq, fh[i]);
+      gemm_frag<MMA>(As[buf] + (wm * 32 + i * 16 + row) * LD + 8 * kq, fa[i]);
+      gemm_frag<MMA>(Hs[buf] + (wq * 32 + i * 16 + row) * LD + 8 * kq, fh[i]);
     }
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
       for (int j = 0; j < 2; ++j) acc[i][j] = mma(fa[i], fh[j], acc[i][j]);
+    if (s + 1 < s_hi) stage(buf ^ 1);
     __syncthreads();
   }
-  float* out = a.part + ((long)split * N + n) * GD * D;
+  float* out = a.part + ((long)split * p.N + n) * GD * p.D;
 #pragma unroll
   for (int i = 0; i < 2; ++i)
 #pragma unroll
     for (int j = 0; j < 2; ++j)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) out[(long)(m0 + i * 16 + 4 * kq + r) * D + q0 + j * 16 + row] = acc[i][j][r];
+      for (int r = 0; r < 4; ++r)
+        out[(long)(m0 + wm * 32 + i * 16 + 4 * kq + r) * p.D + q0 + wq * 32 + j * 16 + row] = acc[i][j][r];
 }
 
 // dR = sum of the split-K partials (layout [n][g*D+o][p] -> [g][n][o][p]);
@@ -161,9 +203,12 @@ __global__ void __launch_bounds__(256) clear_kernel(uint32_t* p, long n) {
   for (long i = blockIdx.x * 256L + threadIdx.x; i < n; i += (long)gridDim.x * 256) p[i] = 0u;
 }
 
-const void* gemm_kernel(int mma) {
-  return mma == MMA_BF16 ? reinterpret_cast<const void*>(&dr_gemm_kernel<MMA_BF16>)
-                         : reinterpret_cast<const void*>(&dr_gemm_kernel<MMA_F32>);
+const void* gemm_kernel(int mma, bool wide) {
+  if (wide)
+    return mma == MMA_BF16 ? reinterpret_cast<const void*>(&dr_gemm_kernel<MMA_BF16, 2, 2>)
+                           : reinterpret_cast<const void*>(&dr_gemm_kernel<MMA_F32, 2, 2>);
+  return mma == MMA_BF16 ? reinterpret_cast<const void*>(&dr_gemm_kernel<MMA_BF16, 1, 1>)
+                         : reinterpret_cast<const void*>(&dr_gemm_kernel<MMA_F32, 1, 1>);
 }
 const void* reduce_kernel() { return reinterpret_cast<const void*>(&dr_reduce_kernel); }
 const void* zero_kernel() { return reinterpret_cast<const void*>(&clear_kernel); }

@@ -84,7 +84,8 @@ inline const void* recurrence_kernel(int cell, int mma, int ks, int ktw, int ndt
   }
   return nullptr;
 }
-const void* gemm_kernel(int mma);
+// dR GEMM: wide = 64x64 workgroup tiles (4 waves, D % 64 == 0), else 32x32 (1 wave).
+const void* gemm_kernel(int mma, bool wide);
 const void* reduce_kernel();
 const void* zero_kernel();
 

@@ -143,85 +143,95 @@ struct Prof {
   }
 };
 
-// Poll the exchange until every 8-word run this wave needs carries `tag`.
-// Runs of padded batch rows are not read (their fragments stay zero).
-// Returns the number of polls.
-template <int MMA, int NB, int NF>
-__device__ __forceinline__ uint32_t gather(const Xchg& x, const int (&word)[NB][NF], const bool (&bval)[NB],
-                                           int off, int nf, uint32_t tag, Frag<MMA> (&X)[NB][NF],
-                                           uint32_t* status, uint32_t spin_limit, bool& abort) {
-  if (abort) return 0;
+// Poll the exchange and run the step's product on it, fused. Every 8-word run
+// of this wave's contraction range is loaded at once; as each arrives it is
+// unpacked, its tags checked, and its MFMAs issued into the caller's
+// accumulators, so the products overlap the tail of the loads. If any tag is
+// stale the accumulators are cleared and the poll repeats. Runs of padded batch
+// rows are not read (they contribute zero). zero() clears the accumulators,
+// prod(bt, j, frag) adds run j of batch tile bt. Returns the number of polls.
+template <int MMA, int NB, int NF, typename Zero, typename Prod>
+__device__ __forceinline__ uint32_t gather_mma(const Xchg& x, const int (&word)[NB][NF], const bool (&bval)[NB],
+                                               int off, int nf, uint32_t tag, uint32_t* status, uint32_t spin_limit,
+                                               bool& abort, Zero zero, Prod prod) {
   uint32_t spins = 0;
   while (true) {
+    zero();
+    if (abort) return spins;
     Run<MMA> r[NB][NF];
 #pragma unroll
     for (int bt = 0; bt < NB; ++bt)
 #pragma unroll
-      for (int j = 0; j < NF; ++j)
+      for (int j = 0; j < NF; ++j) {
+        r[bt][j].zero();
         if (j < nf && bval[bt]) xload<MMA>(x, word[bt][j] + off, r[bt][j]);
+      }
+    // Branch-free from here on: the MFMAs read operands across lanes and must
+    // run with the whole wave active, so lane-dependent conditions are selects.
     bool ok = true;
 #pragma unroll
     for (int bt = 0; bt < NB; ++bt)
 #pragma unroll
       for (int j = 0; j < NF; ++j)
-        if (j < nf && bval[bt]) ok &= xunpack<MMA>(r[bt][j], tag, X[bt][j]);
+        if (j < nf) {
+          Frag<MMA> f;
+          const bool fresh = xunpack<MMA>(r[bt][j], tag, f);
+          ok &= fresh || !bval[bt];
+          prod(bt, j, frag_keep<MMA>(bval[bt], f));
+        }
     ++spins;
     if (__all(ok)) return spins;
     if (spins >= spin_limit) {
       raise_status(status, ST_TIMEOUT);
       abort = true;
-      return spins;
-    }
-    if ((spins & 63u) == 0 && load_status(status) != 0) {
+    } else if ((spins & 63u) == 0 && load_status(status) != 0) {
       abort = true;
-      return spins;
     }
   }
 }
 
-// Paired poll for slabs with at most 8 real batch rows (one 16-row tile): the
-// upper half of each 16-lane row (padding columns of the MFMA operand) polls
-// the odd k-tile of each pair for the same batch row, so a lane issues half the
-// loads; the odd tile then moves down 8 lanes (DPP) and the upper lanes are
-// zeroed. word[j] is the run of k-tile j for batch row lane % 8.
-template <int MMA, int NF>
-__device__ __forceinline__ uint32_t gather_pair(const Xchg& x, const int (&word)[NF], bool bv, int off, int nf,
-                                                uint32_t tag, Frag<MMA> (&X)[1][NF], uint32_t* status,
-                                                uint32_t spin_limit, bool& abort) {
-  if (abort) return 0;
+// Paired variant for slabs with at most 8 real batch rows (one 16-row tile):
+// the upper half of each 16-lane row (padding columns of the MFMA operand)
+// polls the odd k-tile of each pair for the same batch row, so a lane issues
+// half the loads; the odd tile then moves down 8 lanes (DPP) and the upper
+// lanes contribute zero. word[j] is the run of k-tile j for batch row lane % 8.
+template <int MMA, int NF, typename Zero, typename Prod>
+__device__ __forceinline__ uint32_t gather_pair_mma(const Xchg& x, const int (&word)[NF], bool bv, int off, int nf,
+                                                    uint32_t tag, uint32_t* status, uint32_t spin_limit, bool& abort,
+                                                    Zero zero, Prod prod) {
   constexpr int NP = (NF + 1) / 2;
   const int hi = (threadIdx.x >> 3) & 1;  // lane % 16 >= 8
   uint32_t spins = 0;
   while (true) {
+    zero();
+    if (abort) return spins;
     Run<MMA> r[NP];
 #pragma unroll
-    for (int i = 0; i < NP; ++i)
+    for (int i = 0; i < NP; ++i) {
+      r[i].zero();
       if (2 * i + hi < nf && bv) xload<MMA>(x, word[2 * i + hi] + off, r[i]);
+    }
+    // Branch-free from here on (cross-lane DPP and MFMA need the whole wave).
     bool ok = true;
-    Frag<MMA> f[NP];
 #pragma unroll
     for (int i = 0; i < NP; ++i) {
-      f[i].zero();
-      if (2 * i + hi < nf && bv) ok &= xunpack<MMA>(r[i], tag, f[i]);
+      if (2 * i >= nf) continue;
+      const bool v = 2 * i + hi < nf && bv;
+      Frag<MMA> f;
+      const bool fresh = xunpack<MMA>(r[i], tag, f);
+      ok &= fresh || !v;
+      f = frag_keep<MMA>(v, f);
+      const Frag<MMA> odd = frag_rot8(f);
+      prod(0, 2 * i, frag_keep<MMA>(!hi, f));
+      if (2 * i + 1 < nf) prod(0, 2 * i + 1, frag_keep<MMA>(!hi, odd));
     }
     ++spins;
-    if (__all(ok)) {
-#pragma unroll
-      for (int i = 0; i < NP; ++i) {
-        const Frag<MMA> odd = frag_rot8(f[i]);
-        X[0][2 * i] = frag_keep<MMA>(!hi, f[i]);
-        if (2 * i + 1 < NF) X[0][2 * i + 1] = frag_keep<MMA>(!hi, odd);
-      }
-      return spins;
-    }
+    if (__all(ok)) return spins;
     if (spins >= spin_limit) {
       raise_status(status, ST_TIMEOUT);
       abort = true;
-      return spins;
-    }
-    if ((spins & 63u) == 0 && load_status(status) != 0) {
+    } else if ((spins & 63u) == 0 && load_status(status) != 0) {
       abort = true;
-      return spins;
     }
   }
 }
@@ -413,12 +423,6 @@ __global__ void __launch_bounds__(64 * (KSC + 1) * NDT) fwd_kernel(FwdArgs a) {
     for (int g = 0; g < GT; ++g) bias[s][g] = own[s] ? ld_val(a.bias, ((long)g * N + tm.n) * D + el[s].d, p.dt_io) : 0.f;
   }
 
-  Frag<MMA> X[NB][KTW];
-#pragma unroll
-  for (int bt = 0; bt < NB; ++bt)
-#pragma unroll
-    for (int j = 0; j < KTW; ++j) X[bt][j].zero();
-
   Prof prof;
   prof.init(a.prof != nullptr && blockIdx.x == 0);
   // Retire every set-up load before the loop: the wait-count pass then sees no
@@ -427,49 +431,47 @@ __global__ void __launch_bounds__(64 * (KSC + 1) * NDT) fwd_kernel(FwdArgs a) {
   __builtin_amdgcn_s_waitcnt(0);
   bool abort = false;
   for (int t = 0; t < T; ++t) {
-    // ---- 1. h_{t-1} fragments
+    // ---- 1+2. h_{t-1} and the partial R . h over this wave's k-tiles
+    f32x4 acc[NB][GR];
+    auto zero = [&]() {
+#pragma unroll
+      for (int bt = 0; bt < NB; ++bt)
+#pragma unroll
+        for (int g = 0; g < GR; ++g) acc[bt][g] = f32x4{0.f, 0.f, 0.f, 0.f};
+    };
+    auto prod = [&](int bt, int j, const Frag<MMA>& f) {
+#pragma unroll
+      for (int g = 0; g < GR; ++g) acc[bt][g] = mma(A[g][j], f, acc[bt][g]);
+    };
     if (t == 0) {
+      zero();
 #pragma unroll
       for (int bt = 0; bt < NB; ++bt)
 #pragma unroll
         for (int j = 0; j < KTW; ++j)
-          if (j < nkt && bval[bt]) {
-            const int b = tm.slab * p.BS + bt * 16 + tm.row;
-            const long base = ((long)b * N + tm.n) * D + (kt0 + j) * 32 + 8 * tm.kq;
+          if (j < nkt) {
+            Frag<MMA> f;
+            f.zero();
+            if (bval[bt]) {
+              const int b = tm.slab * p.BS + bt * 16 + tm.row;
+              const long base = ((long)b * N + tm.n) * D + (kt0 + j) * 32 + 8 * tm.kq;
 #pragma unroll
-            for (int i = 0; i < 8; ++i) frag_set(X[bt][j], i, ld_val(a.s0, base + i, p.dt_state));
+              for (int i = 0; i < 8; ++i) frag_set(f, i, ld_val(a.s0, base + i, p.dt_state));
+            }
+            prod(bt, j, f);
           }
     } else {
       uint32_t polls;
-      if constexpr (NB == 1) {
-        if (pair)
-          polls = gather_pair<MMA, KTW>(xc, xword_pair, bv_pair, ((t - 1) & 1) * xpar, nkt, step_tag(t - 1), X,
-                                        a.status, a.spin_limit, abort);
-        else
-          polls = gather<MMA, NB, KTW>(xc, xword, bval, ((t - 1) & 1) * xpar, nkt, step_tag(t - 1), X, a.status,
-                                       a.spin_limit, abort);
-      } else {
-        polls = gather<MMA, NB, KTW>(xc, xword, bval, ((t - 1) & 1) * xpar, nkt, step_tag(t - 1), X, a.status,
-                                     a.spin_limit, abort);
-      }
+      const int off = ((t - 1) & 1) * xpar;
+      if (NB == 1 && pair)
+        polls = gather_pair_mma<MMA, KTW>(xc, xword_pair, bv_pair, off, nkt, step_tag(t - 1), a.status, a.spin_limit,
+                                          abort, zero, prod);
+      else
+        polls = gather_mma<MMA, NB, KTW>(xc, xword, bval, off, nkt, step_tag(t - 1), a.status, a.spin_limit, abort,
+                                         zero, prod);
       prof.add(4, polls);
     }
     prof.mark(0);
-
-    // ---- 2. partial R . h over this wave's k-tiles, to LDS
-    f32x4 acc[NB][GR];
-#pragma unroll
-    for (int bt = 0; bt < NB; ++bt)
-#pragma unroll
-      for (int g = 0; g < GR; ++g) acc[bt][g] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int j = 0; j < KTW; ++j)
-      if (j < nkt) {
-#pragma unroll
-        for (int g = 0; g < GR; ++g)
-#pragma unroll
-          for (int bt = 0; bt < NB; ++bt) acc[bt][g] = mma(A[g][j], X[bt][j], acc[bt][g]);
-      }
     float* rp = red + (long)(t & 1) * KS * NB * 1024;
 #pragma unroll
     for (int bt = 0; bt < NB; ++bt)
@@ -739,12 +741,6 @@ __global__ void __launch_bounds__(64 * (KSC + 1) * NDT) bwd_kernel(BwdArgs a) {
     for (int g = 0; g < GT; ++g) dbacc[s][g] = 0.f;
   }
 
-  Frag<MMA> X[NB][NF];
-#pragma unroll
-  for (int bt = 0; bt < NB; ++bt)
-#pragma unroll
-    for (int j = 0; j < NF; ++j) X[bt][j].zero();
-
   Prof prof;
   prof.init(a.prof != nullptr && blockIdx.x == 0);
   __builtin_amdgcn_s_waitcnt(0);  // no set-up load pending at the loop head (see the forward kernel)
@@ -799,27 +795,22 @@ __global__ void __launch_bounds__(64 * (KSC + 1) * NDT) bwd_kernel(BwdArgs a) {
     }
     prof.mark(3);
 
-    // ---- 2. dh_{t-1} partial = R^T dG_t over this wave's k-tiles
+    // ---- 2. dh_{t-1} partial = R^T dG_t over this wave's k-tiles, fused with the poll
+    f32x4 acc[NB];
+    auto zero = [&]() {
+#pragma unroll
+      for (int bt = 0; bt < NB; ++bt) acc[bt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    };
+    auto prod = [&](int bt, int j, const Frag<MMA>& f) { acc[bt] = mma(A[j], f, acc[bt]); };
     uint32_t polls;
-    if constexpr (NB == 1) {
-      if (pair)
-        polls = gather_pair<MMA, NF>(xc, xword_pair, bv_pair, xoff, nkt, step_tag(it), X, a.status, a.spin_limit, abort);
-      else
-        polls = gather<MMA, NB, NF>(xc, xword, bval, xoff, nkt, step_tag(it), X, a.status, a.spin_limit, abort);
-    } else {
-      polls = gather<MMA, NB, NF>(xc, xword, bval, xoff, nkt, step_tag(it), X, a.status, a.spin_limit, abort);
-    }
+    if (NB == 1 && pair)
+      polls = gather_pair_mma<MMA, NF>(xc, xword_pair, bv_pair, xoff, nkt, step_tag(it), a.status, a.spin_limit,
+                                       abort, zero, prod);
+    else
+      polls = gather_mma<MMA, NB, NF>(xc, xword, bval, xoff, nkt, step_tag(it), a.status, a.spin_limit, abort, zero,
+                                      prod);
     prof.add(4, polls);
     prof.mark(0);
-    f32x4 acc[NB];
-#pragma unroll
-    for (int bt = 0; bt < NB; ++bt) acc[bt] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int j = 0; j < NF; ++j)
-      if (j < nkt) {
-#pragma unroll
-        for (int bt = 0; bt < NB; ++bt) acc[bt] = mma(A[j], X[bt][j], acc[bt]);
-      }
     float* rp = red + (long)(it & 1) * NB * 256 * KS;
 #pragma unroll
     for (int bt = 0; bt < NB; ++bt)
