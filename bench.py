@@ -29,6 +29,23 @@ FLOP_PER_LAUNCH = 2.0 * B * T * N * G * D * D  # one recurrent product (fwd), R^
 MI355X_CUS = 256
 
 
+TRAFFIC_FILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
+                            "hbm_traffic_lstm_B8T1024N3D256.txt")
+KERNEL_TAGS = ["fwd_kernel", "bwd_kernel", "dr_gemm_kernel"]
+
+
+def measured_traffic(kernel_tag):
+    """HBM bytes per launch of a kernel from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE summary."""
+    try:
+        for line in open(TRAFFIC_FILE):
+            f = line.split()
+            if len(f) >= 6 and kernel_tag in f[0]:
+                return int(f[-1])
+    except OSError:
+        pass
+    return None
+
+
 def make_inputs(torch, device, seed=20261201):
     g = torch.Generator().manual_seed(seed)
     wx = torch.randn(B, T, G, N, D, generator=g)
@@ -78,6 +95,9 @@ def main(argv=None):
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--phases", action="store_true", help="also report the in-kernel phase profile")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="only run a plain device copy of MIB MiB (5 times): the reference point that scales "
+                         "the FETCH_SIZE / WRITE_SIZE counters to bytes")
     args = ap.parse_args(argv)
     if args.gpus != 1:
         print(
@@ -88,6 +108,16 @@ def main(argv=None):
         return 2
 
     import torch
+
+    if args.copy_calibration:
+        n = args.copy_calibration << 20
+        src = torch.ones(n, dtype=torch.uint8, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_bytes": n, "launches": 5}), flush=True)
+        return 0
 
     sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
     from flashrnn_amd import _lib, flashrnn, synchronize_and_check
@@ -156,7 +186,8 @@ def main(argv=None):
             "frac": round(achieved / PEAK_BF16_TFLOPS, 6),
             "active_cu_frac": round(achieved / (PEAK_BF16_TFLOPS * cus / MI355X_CUS), 5),
             "flop_per_launch": FLOP_PER_LAUNCH,
-            "traffic": None,
+            "traffic": measured_traffic(KERNEL_TAGS[dom]),
+            "traffic_source": os.path.relpath(TRAFFIC_FILE, os.path.dirname(os.path.abspath(__file__))),
         },
     }
     if args.phases:
