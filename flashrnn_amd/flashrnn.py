@@ -6,7 +6,7 @@ on its fused backend: same signature, same public layouts, same return value
 The work runs in ``libfrnn.so`` (hand-written gfx950 HIP kernels) through the
 C ABI of ``include/frnn.h``; PyTorch provides device memory and the stream.
 
-Shapes (``flashrnn.py:46-68``): ``Wx [B,T,G_W,N,D]``, ``R [G_R,N,D,D]`` (output
+Shapes (``flashrnn/flashrnn/flashrnn.py:45-70``): ``Wx [B,T,G_W,N,D]``, ``R [G_R,N,D,D]`` (output
 index before input index), ``b [G_T,N,D]``, ``states [S,B,1,N,D]``; per cell
 ``(G_R, G_W, G_T, S)`` = lstm (4,4,4,2), slstm (4,4,4,4), gru (3,3,4,1),
 elman (1,1,1,1).
@@ -35,7 +35,7 @@ import torch.nn.functional as F
 
 from . import _lib
 
-# (G_R, G_W, G_T, S); rnn_function_registry, flashrnn.py:46-68
+# (G_R, G_W, G_T, S); rnn_function_registry, flashrnn/flashrnn/flashrnn.py:45-70
 CELL_SIZES = {"lstm": (4, 4, 4, 2), "slstm": (4, 4, 4, 4), "gru": (3, 3, 4, 1), "elman": (1, 1, 1, 1)}
 FUSED_BACKENDS = ("cuda_fused", "fused", "hip_fused")
 DTYPES = {"bfloat16": torch.bfloat16, "float32": torch.float32}
@@ -44,7 +44,7 @@ _IO = {torch.float32: _lib.FRNN_F32, torch.bfloat16: _lib.FRNN_BF16}
 
 @dataclass
 class FlashRNNConfig:
-    """The subset of the reference's ``FlashRNNConfig`` (``flashrnn.py:121-380``)
+    """The subset of the reference's ``FlashRNNConfig`` (``flashrnn/flashrnn/flashrnn.py:121-380``)
     that applies to the fused path. Options of the reference that this build
     does not implement yet raise ``NotImplementedError`` instead of being ignored."""
 
@@ -134,7 +134,7 @@ def _desc(cell, B, T, N, D, io, st, mma, training):
 
 class _FusedRecurrence(torch.autograd.Function):
     """Autograd contract of the reference's FlashRNNFunctionFused
-    (``flashrnn.py:697-802``): saves what the backward kernel needs, returns
+    (``flashrnn/flashrnn/flashrnn.py:697-802``): saves what the backward kernel needs, returns
     gradients for Wx, R, b and the initial state."""
 
     @staticmethod

@@ -77,7 +77,7 @@ enum frnn_status {
   FRNN_E_PLACEMENT = -6,   /* device: a workgroup ran on an unexpected XCD */
 };
 
-/* Gate and state counts of a cell: (G_R, G_W, G_T, S); flashrnn.py:46-68. */
+/* Gate and state counts of a cell: (G_R, G_W, G_T, S); flashrnn/flashrnn/flashrnn.py:45-70. */
 int frnn_cell_sizes(int cell, int32_t* g_r, int32_t* g_w, int32_t* g_t, int32_t* s);
 
 /* Bytes of the caller-owned areas. which: 0 = forward workspace,

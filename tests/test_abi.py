@@ -1,0 +1,140 @@
+"""The C ABI of libfrnn.so and the host-side contract, without a GPU.
+
+Covers: every function include/frnn.h declares is exported and bound; cell
+gate/state counts equal the reference's registry (flashrnn/flashrnn/flashrnn.py:45-70);
+plan and workspace sizing; argument validation that returns before any device
+call; and the Python front end's shape/config errors (flashrnn/flashrnn/flashrnn.py
+FlashRNNConfig and flashrnn()).
+"""
+
+import ctypes
+import pathlib
+import re
+
+import pytest
+import torch
+
+from flashrnn_amd import _lib
+from flashrnn_amd.flashrnn import CELL_SIZES, FlashRNNConfig, flashrnn
+from oracle.torch_restatement import SIZES as ORACLE_SIZES
+
+HEADER = pathlib.Path(__file__).resolve().parents[1] / "include" / "frnn.h"
+
+
+def declared_functions():
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return sorted(set(re.findall(r"^\s*[A-Za-z_][\w\s\*]*?\b(frnn_\w+)\s*\(", text, flags=re.M)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    return _lib.load()
+
+
+def desc(cell="lstm", B=8, T=1024, N=3, D=256, io=_lib.FRNN_BF16, st=_lib.FRNN_F32, mma=_lib.FRNN_MMA_BF16,
+         flags=_lib.FRNN_TRAINING):
+    return _lib.FrnnDesc(_lib.CELLS[cell], B, T, N, D, io, st, mma, flags)
+
+
+def test_header_declares_the_bound_exports():
+    assert declared_functions() == sorted(_lib.EXPORTS)
+
+
+def test_library_exports_every_declared_symbol(lib):
+    for name in declared_functions():
+        assert hasattr(lib, name), name
+
+
+@pytest.mark.parametrize("cell", ["lstm", "gru", "elman", "slstm"])
+def test_cell_sizes_match_reference_registry(lib, cell):
+    out = [ctypes.c_int32() for _ in range(4)]
+    assert lib.frnn_cell_sizes(_lib.CELLS[cell], *[ctypes.byref(o) for o in out]) == _lib.FRNN_OK
+    assert tuple(o.value for o in out) == CELL_SIZES[cell]
+    assert CELL_SIZES[cell][1:] == ORACLE_SIZES[cell]
+
+
+def test_cell_sizes_rejects_unknown_cell(lib):
+    out = [ctypes.c_int32() for _ in range(4)]
+    assert lib.frnn_cell_sizes(17, *[ctypes.byref(o) for o in out]) == -1
+
+
+def test_workspace_sizes(lib):
+    d = desc()
+    ws_f, ws_b, save = (lib.frnn_workspace_bytes(ctypes.byref(d), w) for w in range(3))
+    assert ws_f > 0 and ws_b > 0 and save > 0
+    # the saved activations grow linearly in T; the exchange workspace does not depend on T
+    d2 = desc(T=2048)
+    assert lib.frnn_workspace_bytes(ctypes.byref(d2), 2) == 2 * save
+    assert lib.frnn_workspace_bytes(ctypes.byref(d2), 0) == ws_f
+    # saved activations hold at least one FP32 value per real element and step
+    assert save >= 8 * 1024 * 3 * 256 * 4
+    assert lib.frnn_workspace_bytes(ctypes.byref(d), 7) == 0
+
+
+@pytest.mark.parametrize(
+    "kw",
+    [dict(B=0), dict(T=0), dict(N=0), dict(D=0), dict(io=5), dict(st=9), dict(mma=4)],
+)
+def test_invalid_descriptors(lib, kw):
+    d = desc(**kw)
+    assert lib.frnn_workspace_bytes(ctypes.byref(d), 0) == 0
+    assert lib.frnn_fwd(ctypes.byref(d), *([None] * 8), 0, None) == -1
+
+
+@pytest.mark.parametrize("D", [20, 1056, 2048])
+def test_unsupported_widths(lib, D):
+    d = desc(D=D)
+    assert lib.frnn_workspace_bytes(ctypes.byref(d), 0) == 0
+    assert lib.frnn_fwd(ctypes.byref(d), *([None] * 8), 0, None) == -2
+
+
+def test_null_pointers_rejected_before_launch(lib):
+    d = desc(B=2, T=4, N=1, D=64)
+    assert lib.frnn_fwd(ctypes.byref(d), *([None] * 8), 0, None) == -1
+    assert lib.frnn_bwd(ctypes.byref(d), *([None] * 11), 0, None) == -1
+    assert lib.frnn_status(None, None) == -1
+
+
+def test_strerror_names_every_code(lib):
+    seen = set()
+    for code in range(0, -7, -1):
+        s = lib.frnn_strerror(code)
+        assert s and s not in seen
+        seen.add(s)
+
+
+def test_missing_library_fails_loudly(tmp_path):
+    with pytest.raises(RuntimeError, match="no fallback"):
+        _lib.load(tmp_path / "libfrnn.so")
+
+
+# ----------------------------------------------------------------- Python front end
+def test_config_validation():
+    with pytest.raises(ValueError):
+        FlashRNNConfig(function="transformer")
+    with pytest.raises(ValueError):
+        FlashRNNConfig(backend="vanilla")
+    with pytest.raises(ValueError):
+        FlashRNNConfig(dtype="float16")
+    with pytest.raises(NotImplementedError):
+        FlashRNNConfig(gradient_recurrent_clipval=1.0)
+    c = FlashRNNConfig(function="slstm")
+    assert (c.num_gates_r, c.num_gates_w, c.num_gates_t, c.num_states) == (4, 4, 4, 4)
+
+
+def test_shape_errors_and_cpu_tensors():
+    B, T, N, D = 2, 3, 1, 32
+    wx = torch.zeros(B, T, 4, N, D)
+    R = torch.zeros(4, N, D, D)
+    b = torch.zeros(4, N, D)
+    s0 = torch.zeros(2, B, 1, N, D)
+    with pytest.raises(ValueError, match="gates"):
+        flashrnn(wx[:, :, :3], R, b, s0, function="lstm")
+    with pytest.raises(ValueError, match="recurrent weights"):
+        flashrnn(wx, R[:, :, :, :16], b, s0, function="lstm")
+    with pytest.raises(ValueError, match="bias"):
+        flashrnn(wx, R, b[:3], s0, function="lstm")
+    with pytest.raises(ValueError, match="initial state"):
+        flashrnn(wx, R, b, s0[:1], function="lstm")
+    with pytest.raises(ValueError, match="device tensors"):
+        flashrnn(wx, R, b, s0, function="lstm")
