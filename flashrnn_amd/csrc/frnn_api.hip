@@ -19,7 +19,8 @@ namespace {
 
 using frnn::Plan;
 
-std::atomic<uint32_t> g_spin_limit{1u << 22};
+constexpr uint32_t kDefaultSpinLimit = 1u << 22;
+std::atomic<uint32_t> g_spin_limit{kDefaultSpinLimit};
 std::atomic<unsigned long long*> g_phase_prof{nullptr};
 
 // ---- optional kernel timing (frnn_timing_enable / frnn_timing_read)
@@ -92,6 +93,13 @@ int ktw_class(int need, int ndt) {
   return 0;
 }
 
+// Groups [g0, g0 + n) form one launch; its grid in either placement mode.
+void set_groups(Plan* p, int g0, int n) {
+  p->g0 = g0;
+  p->gcount = n;
+  p->grid = (p->flags & FRNN_XCD_SHARED) ? n * p->wpg : frnn::kXcds * p->wpg * ((n + frnn::kXcds - 1) / frnn::kXcds);
+}
+
 int make_plan(const frnn_desc* d, Plan* p) {
   if (!d) return FRNN_E_INVALID;
   std::memset(p, 0, sizeof(*p));
@@ -144,8 +152,7 @@ int make_plan(const frnn_desc* d, Plan* p) {
   p->epl = (4 * p->NB + p->KS - 1) / p->KS;
   p->nsave = nsave_of(p->cell);
   p->wpg = p->D / (16 * p->NDT);
-  p->grid = (p->flags & FRNN_XCD_SHARED) ? p->ngroups * p->wpg
-                                         : frnn::kXcds * p->wpg * ((p->ngroups + frnn::kXcds - 1) / frnn::kXcds);
+  set_groups(p, 0, p->ngroups);
   p->nwg = p->ngroups * p->wpg;
   const long long wsz = p->mma == FRNN_MMA_BF16 ? 4 : 8;
   p->xwords_fwd = (long long)p->ngroups * p->BS * p->D;
@@ -193,9 +200,11 @@ int set_lds_limit(const void* fn, size_t lds) {
   return FRNN_OK;
 }
 
-// The persistent kernels need every active workgroup of a group resident at
-// once. Check that the busiest XCD (or, placement-free, the GPU) can hold them.
-int check_residency(const Plan& p, const void* fn, int block, size_t lds) {
+// The persistent kernels need every workgroup of a group resident at once
+// (groups never wait on each other). Return in *per_launch how many groups one
+// launch may hold: what the GPU holds placement-free, or with every group on
+// one XCD, eight times what the busiest XCD holds.
+int groups_per_launch(const Plan& p, const void* fn, int block, size_t lds, int* per_launch) {
   int dev = 0, cus = 0, per_cu = 0;
   if (hipGetDevice(&dev) != hipSuccess) return FRNN_E_LAUNCH;
   if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return FRNN_E_LAUNCH;
@@ -203,15 +212,26 @@ int check_residency(const Plan& p, const void* fn, int block, size_t lds) {
     (void)hipGetLastError();
     return FRNN_E_LAUNCH;
   }
-  long long need, have;
-  if (p.flags & FRNN_XCD_SHARED) {
-    need = (long long)p.ngroups * p.wpg;
-    have = (long long)cus * per_cu;
-  } else {
-    need = (long long)((p.ngroups + frnn::kXcds - 1) / frnn::kXcds) * p.wpg;
-    have = (long long)(cus / frnn::kXcds) * per_cu;
+  long long g;
+  if (p.flags & FRNN_XCD_SHARED)
+    g = (long long)cus * per_cu / p.wpg;
+  else
+    g = (long long)frnn::kXcds * ((long long)(cus / frnn::kXcds) * per_cu / p.wpg);
+  if (g < 1) return FRNN_E_UNSUPPORTED;
+  *per_launch = (int)std::min<long long>(g, p.ngroups);
+  return FRNN_OK;
+}
+
+// Launch the persistent kernel over all groups in as few launches as residency
+// allows; `ap` is the plan inside the kernel arguments `arg`.
+int launch_groups(Plan* ap, const void* fn, int block, size_t lds, void* arg, int per_launch, hipStream_t st) {
+  int rc = FRNN_OK;
+  for (int g0 = 0; g0 < ap->ngroups && rc == FRNN_OK; g0 += per_launch) {
+    set_groups(ap, g0, std::min(per_launch, ap->ngroups - g0));
+    rc = launch(fn, ap->grid, block, lds, arg, st);
   }
-  return need <= have ? FRNN_OK : FRNN_E_UNSUPPORTED;
+  set_groups(ap, 0, ap->ngroups);
+  return rc;
 }
 
 int clear(void* base, long long bytes, hipStream_t stream) {
@@ -287,11 +307,12 @@ int frnn_fwd(const frnn_desc* d, const void* wx, const void* R, const void* b, c
   a.prof = g_phase_prof.load();
   const size_t lds = (size_t)p.NDT * frnn::recurrence_lds_floats(p.cell, true, p.KS) * sizeof(float);
   const int block = 64 * p.NDT * (p.KS + 1);
+  int per_launch = 0;
   if ((rc = set_lds_limit(fn, lds)) != FRNN_OK) return rc;
-  if ((rc = check_residency(p, fn, block, lds)) != FRNN_OK) return rc;
+  if ((rc = groups_per_launch(p, fn, block, lds, &per_launch)) != FRNN_OK) return rc;
   hipEvent_t t0;
   const bool timed = timing_begin(st, &t0);
-  rc = launch(fn, p.grid, block, lds, &a, st);
+  rc = launch_groups(&a.p, fn, block, lds, &a, per_launch, st);
   if (timed) timing_end(0, t0, st);
   return rc;
 }
@@ -328,11 +349,12 @@ int frnn_bwd(const frnn_desc* d, const void* R, const void* s0, const void* stat
   a.prof = g_phase_prof.load();
   const size_t lds = (size_t)p.NDT * frnn::recurrence_lds_floats(p.cell, false, p.KSB) * sizeof(float);
   const int block = 64 * p.NDT * (p.KSB + 1);
+  int per_launch = 0;
   if ((rc = set_lds_limit(fn, lds)) != FRNN_OK) return rc;
-  if ((rc = check_residency(p, fn, block, lds)) != FRNN_OK) return rc;
+  if ((rc = groups_per_launch(p, fn, block, lds, &per_launch)) != FRNN_OK) return rc;
   hipEvent_t t0;
   bool timed = timing_begin(st, &t0);
-  rc = launch(fn, p.grid, block, lds, &a, st);
+  rc = launch_groups(&a.p, fn, block, lds, &a, per_launch, st);
   if (timed) timing_end(1, t0, st);
   if (rc != FRNN_OK) return rc;
 
@@ -408,6 +430,6 @@ void frnn_set_phase_profile(void* device_words) {
   g_phase_prof.store(static_cast<unsigned long long*>(device_words));
 }
 
-void frnn_set_spin_limit(uint32_t polls) { g_spin_limit.store(polls ? polls : 1u); }
+void frnn_set_spin_limit(uint32_t polls) { g_spin_limit.store(polls ? polls : kDefaultSpinLimit); }
 
 }  // extern "C"

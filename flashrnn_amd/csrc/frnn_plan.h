@@ -29,7 +29,9 @@ struct Plan {
   int KS;          // forward: compute waves per hidden tile (contraction split)
   int KSB;         // backward: compute waves per hidden tile
   int NDT;         // hidden tiles per workgroup (workgroup = NDT * KS waves)
-  int grid;        // launched workgroups (idle ones exit at once)
+  int grid;        // launched workgroups of one launch (idle ones exit at once)
+  int g0, gcount;  // groups [g0, g0 + gcount) run in this launch (launches run in turn when
+                   // all groups cannot be resident at once; groups never wait on each other)
   int nwg;         // active workgroups = ngroups * wpg
   int kt_fwd;      // D / 32
   int kt_bwd;      // GR * D / 32
@@ -50,17 +52,19 @@ struct Plan {
 __host__ __device__
 #endif
 inline bool wg_decode(const Plan& p, int wg, int* group, int* member) {
+  int local;
   if (p.flags & 2) {  // placement-free exchange: compact grid
-    *group = wg / p.wpg;
+    local = wg / p.wpg;
     *member = wg % p.wpg;
-    return *group < p.ngroups;
+  } else {
+    const int xcd = wg % kXcds;
+    const int idx = wg / kXcds;
+    const int slot = idx / p.wpg;
+    *member = idx % p.wpg;
+    local = slot * kXcds + xcd;
   }
-  const int xcd = wg % kXcds;
-  const int idx = wg / kXcds;
-  const int slot = idx / p.wpg;
-  *member = idx % p.wpg;
-  *group = slot * kXcds + xcd;
-  return *group < p.ngroups;
+  *group = p.g0 + local;
+  return local < p.gcount;
 }
 
 }  // namespace frnn

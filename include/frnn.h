@@ -130,7 +130,7 @@ int frnn_timing_read(double* ms3, int32_t* counts3);
  * [5] steps. NULL disables. */
 void frnn_set_phase_profile(void* device_words);
 
-/* Test hook: the spin limit of the exchange waits (default 1<<22 polls).
+/* Test hook: the spin limit of the exchange waits (default 1<<22 polls; 0 restores it).
  * A tiny value forces FRNN_E_TIMEOUT from the host without faulting. */
 void frnn_set_spin_limit(uint32_t polls);
 
