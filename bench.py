@@ -95,6 +95,8 @@ def main(argv=None):
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--phases", action="store_true", help="also report the in-kernel phase profile")
+    ap.add_argument("--trace-out", default=None, help="with --phases: save the per-wave step timelines "
+                    "[fwd/bwd][workgroup][wave][step][stamp] (100 MHz clock) as .npy")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a plain device copy of MIB MiB (5 times): the reference point that scales "
                          "the FETCH_SIZE / WRITE_SIZE counters to bytes")
@@ -191,7 +193,7 @@ def main(argv=None):
         },
     }
     if args.phases:
-        prof = torch.zeros(256, dtype=torch.int64, device=dev)
+        prof = torch.zeros(256 + 2 * 128 * 16 * 64, dtype=torch.int64, device=dev)
         lib.frnn_set_phase_profile(prof.data_ptr())
         step()
         torch.cuda.synchronize()
@@ -210,6 +212,9 @@ def main(argv=None):
                 waves.append({k: round(row[i] / row[5], 1) for i, k in enumerate(keys) if k})
             out[d] = waves
         result["phases_cycles_per_step"] = out
+        if args.trace_out:
+            import numpy as np
+            np.save(args.trace_out, np.array(v[256:], dtype=np.int64).reshape(2, 128, 16, 16, 4))
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(torch)
     print(json.dumps(result), flush=True)

@@ -119,14 +119,33 @@ __device__ __forceinline__ long save_index(const Plan& p, int ne, int t, int wgi
 // [3] owners' cell work (backward: pointwise), [4] exchange polls, [5] steps,
 // [6] backward: reduction of the partial cotangents. I/O waves: [0] ring fill
 // (waits for its loads), [1] load issue, [2] barrier, [3] output drain, [5] steps.
+//
+// With profiling on, every wave of every workgroup also keeps a timeline of
+// steps kTraceT0 .. kTraceT0+15: four stamps per step from the chip-wide
+// 100 MHz clock (s_memrealtime), lane `slot` holding stamp `slot`, written
+// after the loop to trace[(workgroup * 16 + wave) * 64 + lane].
+constexpr int kTraceT0 = 64;
 struct Prof {
   unsigned long long acc[8];
   unsigned long long t;
-  bool on;
-  __device__ __forceinline__ void init(bool enable) {
+  unsigned long long tv;
+  bool on, tr;
+  __device__ __forceinline__ void init(bool enable, bool trace = false) {
     on = enable;
+    tr = trace;
+    tv = 0;
     for (int i = 0; i < 8; ++i) acc[i] = 0;
     t = on ? clock64() : 0;
+  }
+  __device__ __forceinline__ void stamp(int step, int k) {
+    if (!tr) return;
+    const int slot = (step - kTraceT0) * 4 + k;
+    if (slot < 0 || slot >= 64) return;
+    const unsigned long long now = __builtin_amdgcn_s_memrealtime();
+    if ((int)(threadIdx.x & 63) == slot) tv = now;
+  }
+  __device__ __forceinline__ void flush_trace(unsigned long long* trace) {
+    if (tr && blockIdx.x < 128) trace[(blockIdx.x * 16 + (threadIdx.x >> 6)) * 64 + (threadIdx.x & 63)] = tv;
   }
   __device__ __forceinline__ void mark(int k) {
     if (!on) return;
@@ -152,7 +171,7 @@ struct Prof {
 // prod(bt, j, frag) adds run j of batch tile bt. Returns the number of polls.
 template <int MMA, int NB, int NF, typename Zero, typename Prod>
 __device__ __forceinline__ uint32_t gather_mma(const Xchg& x, const int (&word)[NB][NF], const bool (&bval)[NB],
-                                               int off, int nf, uint32_t tag, uint32_t* status, uint32_t spin_limit,
+                                               int off, int cstride, int nf, uint32_t tag, uint32_t* status, uint32_t spin_limit,
                                                bool& abort, Zero zero, Prod prod) {
   uint32_t spins = 0;
   while (true) {
@@ -164,7 +183,7 @@ __device__ __forceinline__ uint32_t gather_mma(const Xchg& x, const int (&word)[
 #pragma unroll
       for (int j = 0; j < NF; ++j) {
         r[bt][j].zero();
-        if (j < nf && bval[bt]) xload<MMA>(x, word[bt][j] + off, r[bt][j]);
+        if (j < nf && bval[bt]) xload<MMA>(x, word[bt][j] + off, cstride, r[bt][j]);
       }
     // Branch-free from here on: the MFMAs read operands across lanes and must
     // run with the whole wave active, so lane-dependent conditions are selects.
@@ -196,7 +215,7 @@ __device__ __forceinline__ uint32_t gather_mma(const Xchg& x, const int (&word)[
 // half the loads; the odd tile then moves down 8 lanes (DPP) and the upper
 // lanes contribute zero. word[j] is the run of k-tile j for batch row lane % 8.
 template <int MMA, int NF, typename Zero, typename Prod>
-__device__ __forceinline__ uint32_t gather_pair_mma(const Xchg& x, const int (&word)[NF], bool bv, int off, int nf,
+__device__ __forceinline__ uint32_t gather_pair_mma(const Xchg& x, const int (&word)[NF], bool bv, int off, int cstride, int nf,
                                                     uint32_t tag, uint32_t* status, uint32_t spin_limit, bool& abort,
                                                     Zero zero, Prod prod) {
   constexpr int NP = (NF + 1) / 2;
@@ -209,7 +228,7 @@ __device__ __forceinline__ uint32_t gather_pair_mma(const Xchg& x, const int (&w
 #pragma unroll
     for (int i = 0; i < NP; ++i) {
       r[i].zero();
-      if (2 * i + hi < nf && bv) xload<MMA>(x, word[2 * i + hi] + off, r[i]);
+      if (2 * i + hi < nf && bv) xload<MMA>(x, word[2 * i + hi] + off, cstride, r[i]);
     }
     // Branch-free from here on (cross-lane DPP and MFMA need the whole wave).
     bool ok = true;
@@ -291,7 +310,7 @@ __device__ void fwd_io(const FwdArgs& a, const Team& tm, float* xring, float* os
   };
 
   Prof prof;
-  prof.init(a.prof != nullptr && blockIdx.x == 0);
+  prof.init(a.prof != nullptr && blockIdx.x == 0, a.prof != nullptr);
   u32x4 buf[P][IOQ][GW];
 #pragma unroll
   for (int j = 0; j < P; ++j)
@@ -319,12 +338,16 @@ __device__ void fwd_io(const FwdArgs& a, const Team& tm, float* xring, float* os
           }
         }
         prof.mark(0);
+        prof.stamp(t, 0);
         if (t + P < T) load_wx(t + P, buf[j]);
         prof.mark(1);
+        prof.stamp(t, 1);
         __syncthreads();  // step t: Wx_t staged; outputs of step t-1 complete
         prof.mark(2);
+        prof.stamp(t, 2);
         if (t >= 1) store_out(t - 1, ost + ((t - 1) & 1) * NOP * NE);
         prof.mark(3);
+        prof.stamp(t, 3);
       }
     }
   }
@@ -332,6 +355,7 @@ __device__ void fwd_io(const FwdArgs& a, const Team& tm, float* xring, float* os
   store_out(T - 1, ost + ((T - 1) & 1) * NOP * NE);
   prof.acc[5] = T;
   prof.flush(a.prof);
+  if (a.prof) prof.flush_trace(a.prof + 256);
 }
 
 template <int CELL, int MMA, int KTW, int NB, int NDT, int KSC>
@@ -388,6 +412,8 @@ __global__ void __launch_bounds__(64 * (KSC + 1) * NDT) fwd_kernel(FwdArgs a) {
     }
 
   // ---- exchange word index of every run this wave reads (h_{t-1}[b][k])
+  const int xgrp = tm.group * p.BS * D;  // this group's table
+  const int cstride = 16 * p.BS;        // bytes between the chunks of a run
   int xword[NB][KTW];
   bool bval[NB];
 #pragma unroll
@@ -395,14 +421,14 @@ __global__ void __launch_bounds__(64 * (KSC + 1) * NDT) fwd_kernel(FwdArgs a) {
     const int bl = bt * 16 + tm.row;
     bval[bt] = tm.slab * p.BS + bl < B;
 #pragma unroll
-    for (int j = 0; j < KTW; ++j) xword[bt][j] = (tm.group * p.BS + bl) * D + (kt0 + j) * 32 + 8 * tm.kq;
+    for (int j = 0; j < KTW; ++j) xword[bt][j] = xgrp + xword_of<MMA>(p.BS, bl, (kt0 + j) * 32 + 8 * tm.kq);
   }
   const int xpar = p.ngroups * p.BS * D;  // words per parity
   // paired-poll runs (slab of <= 8 real rows, see gather_pair)
   const bool pair = NB == 1 && B <= 8;
   int xword_pair[KTW];
 #pragma unroll
-  for (int j = 0; j < KTW; ++j) xword_pair[j] = (tm.group * p.BS + (tm.lane & 7)) * D + (kt0 + j) * 32 + 8 * tm.kq;
+  for (int j = 0; j < KTW; ++j) xword_pair[j] = xgrp + xword_of<MMA>(p.BS, tm.lane & 7, (kt0 + j) * 32 + 8 * tm.kq);
   const bool bv_pair = (tm.lane & 7) < B;
 
   // ---- owned elements
@@ -424,13 +450,14 @@ __global__ void __launch_bounds__(64 * (KSC + 1) * NDT) fwd_kernel(FwdArgs a) {
   }
 
   Prof prof;
-  prof.init(a.prof != nullptr && blockIdx.x == 0);
+  prof.init(a.prof != nullptr && blockIdx.x == 0, a.prof != nullptr);
   // Retire every set-up load before the loop: the wait-count pass then sees no
   // load still pending at the loop head, and does not fence the exchange
   // stores inside the loop behind one.
   __builtin_amdgcn_s_waitcnt(0);
   bool abort = false;
   for (int t = 0; t < T; ++t) {
+    prof.stamp(t, 0);
     // ---- 1+2. h_{t-1} and the partial R . h over this wave's k-tiles
     f32x4 acc[NB][GR];
     auto zero = [&]() {
@@ -464,14 +491,15 @@ __global__ void __launch_bounds__(64 * (KSC + 1) * NDT) fwd_kernel(FwdArgs a) {
       uint32_t polls;
       const int off = ((t - 1) & 1) * xpar;
       if (NB == 1 && pair)
-        polls = gather_pair_mma<MMA, KTW>(xc, xword_pair, bv_pair, off, nkt, step_tag(t - 1), a.status, a.spin_limit,
+        polls = gather_pair_mma<MMA, KTW>(xc, xword_pair, bv_pair, off, cstride, nkt, step_tag(t - 1), a.status, a.spin_limit,
                                           abort, zero, prod);
       else
-        polls = gather_mma<MMA, NB, KTW>(xc, xword, bval, off, nkt, step_tag(t - 1), a.status, a.spin_limit, abort,
+        polls = gather_mma<MMA, NB, KTW>(xc, xword, bval, off, cstride, nkt, step_tag(t - 1), a.status, a.spin_limit, abort,
                                          zero, prod);
       prof.add(4, polls);
     }
     prof.mark(0);
+    prof.stamp(t, 1);
     float* rp = red + (long)(t & 1) * KS * NB * 1024;
 #pragma unroll
     for (int bt = 0; bt < NB; ++bt)
@@ -485,6 +513,7 @@ __global__ void __launch_bounds__(64 * (KSC + 1) * NDT) fwd_kernel(FwdArgs a) {
     prof.mark(1);
     __syncthreads();
     prof.mark(2);
+    prof.stamp(t, 2);
 
     // ---- 3. owners: gates, cell, staged outputs, exchange
     const float* xr = xring + (long)(t % kFwdRing) * NE * GWP;
@@ -534,9 +563,10 @@ __global__ void __launch_bounds__(64 * (KSC + 1) * NDT) fwd_kernel(FwdArgs a) {
         *reinterpret_cast<f32x4*>(os + e * NOP + 4 * c) = f32x4{outv[4 * c], outv[4 * c + 1], outv[4 * c + 2], outv[4 * c + 3]};
       // the exchange word goes out last: nothing after it in this step waits for its completion
       if (el[s].real && t + 1 < T)
-        xstore<MMA>(xc, (t & 1) * xpar + ((long)tm.group * p.BS + el[s].bl) * D + el[s].d, st[s][0], step_tag(t));
+        xstore<MMA>(xc, (t & 1) * xpar + xgrp + xword_of<MMA>(p.BS, el[s].bl, el[s].d), st[s][0], step_tag(t));
     }
     prof.mark(3);
+    prof.stamp(t, 3);
 
   }
   __syncthreads();  // the I/O wave drains the last step
@@ -552,6 +582,7 @@ __global__ void __launch_bounds__(64 * (KSC + 1) * NDT) fwd_kernel(FwdArgs a) {
   }
   prof.acc[5] = T;
   prof.flush(a.prof);
+  if (a.prof) prof.flush_trace(a.prof + 256);
 }
 
 // ===================================================================== backward
@@ -625,7 +656,7 @@ __device__ void bwd_io(const BwdArgs& a, const Team& tm, float* iring, float* os
   };
 
   Prof prof;
-  prof.init(a.prof != nullptr && blockIdx.x == 0);
+  prof.init(a.prof != nullptr && blockIdx.x == 0, a.prof != nullptr);
   u32x4 buf[P][IOQ][NIN];
 #pragma unroll
   for (int j = 0; j < P; ++j)
@@ -642,18 +673,23 @@ __device__ void bwd_io(const BwdArgs& a, const Team& tm, float* iring, float* os
         if (it + 1 < T) {
           stage(jn, buf[jn]);
           prof.mark(0);
+          prof.stamp(it, 0);
           if (it + 1 + P < T) load_in(it + 1 + P, buf[jn]);
           prof.mark(1);
+          prof.stamp(it, 1);
         }
         __syncthreads();  // iteration it: outputs staged; inputs of it+1 staged
         prof.mark(2);
+        prof.stamp(it, 2);
         store_out(it, ost + (long)(it & 1) * NOB * NE);
         prof.mark(3);
+        prof.stamp(it, 3);
       }
     }
   }
   prof.acc[5] = T;
   prof.flush(a.prof ? a.prof + 128 : nullptr);
+  if (a.prof) prof.flush_trace(a.prof + 256 + 128 * 16 * 64);
 }
 
 template <int CELL, int MMA, int KTW, int NB, int NDT, int KSC>
@@ -705,6 +741,8 @@ __global__ void __launch_bounds__(64 * (KSC + 1) * NDT) bwd_kernel(BwdArgs a) {
     }
   }
 
+  const int xgrp = tm.group * p.BS * GD;  // this group's table
+  const int cstride = 16 * p.BS;         // bytes between the chunks of a run
   int xword[NB][NF];
   bool bval[NB];
 #pragma unroll
@@ -712,13 +750,13 @@ __global__ void __launch_bounds__(64 * (KSC + 1) * NDT) bwd_kernel(BwdArgs a) {
     const int bl = bt * 16 + tm.row;
     bval[bt] = tm.slab * p.BS + bl < B;
 #pragma unroll
-    for (int j = 0; j < NF; ++j) xword[bt][j] = (tm.group * p.BS + bl) * GD + (kt0 + j) * 32 + 8 * tm.kq;
+    for (int j = 0; j < NF; ++j) xword[bt][j] = xgrp + xword_of<MMA>(p.BS, bl, (kt0 + j) * 32 + 8 * tm.kq);
   }
   const int xpar = p.ngroups * p.BS * GD;
   const bool pair = NB == 1 && B <= 8;
   int xword_pair[NF];
 #pragma unroll
-  for (int j = 0; j < NF; ++j) xword_pair[j] = (tm.group * p.BS + (tm.lane & 7)) * GD + (kt0 + j) * 32 + 8 * tm.kq;
+  for (int j = 0; j < NF; ++j) xword_pair[j] = xgrp + xword_of<MMA>(p.BS, tm.lane & 7, (kt0 + j) * 32 + 8 * tm.kq);
   const bool bv_pair = (tm.lane & 7) < B;
 
   int oe[EPLMAX];
@@ -742,11 +780,12 @@ __global__ void __launch_bounds__(64 * (KSC + 1) * NDT) bwd_kernel(BwdArgs a) {
   }
 
   Prof prof;
-  prof.init(a.prof != nullptr && blockIdx.x == 0);
+  prof.init(a.prof != nullptr && blockIdx.x == 0, a.prof != nullptr);
   __builtin_amdgcn_s_waitcnt(0);  // no set-up load pending at the loop head (see the forward kernel)
   __syncthreads();  // iteration 0's inputs staged by the I/O wave
   bool abort = false;
   for (int it = 0; it < T; ++it) {
+    prof.stamp(it, 0);
     const int xoff = (it & 1) * xpar;
     // ---- 1. owners: pointwise backward of step t = T-1-it, publish dG_t
     const float* ir = iring + (long)(it % P) * NE * NOP;
@@ -789,11 +828,19 @@ __global__ void __launch_bounds__(64 * (KSC + 1) * NDT) bwd_kernel(BwdArgs a) {
       for (int g = 0; g < GW; ++g) ov[g] = dwx[g];
       if constexpr (CELL == CELL_GRU) ov[3] = dry[0];
       *reinterpret_cast<f32x4*>(os + e * NOB) = ov;
-      // the element's gate cotangents go out last, as one vector store (layout [b][o][g])
-      if (el[s].real)
-        xstore_vec<MMA, GR>(xc, xoff + (((long)tm.group * p.BS + el[s].bl) * D + el[s].d) * GR, dry, step_tag(it));
+      // the element's gate cotangents go out last (k = o * GR + g: one vector store when GR = 4)
+      if (el[s].real) {
+        if constexpr (MMA == MMA_BF16 && GR == 4) {  // k = 4d .. 4d+3: one aligned chunk
+          xstore_vec<MMA, GR>(xc, xoff + xgrp + xword_of<MMA>(p.BS, el[s].bl, el[s].d * GR), dry, step_tag(it));
+        } else {
+#pragma unroll
+          for (int g = 0; g < GR; ++g)
+            xstore<MMA>(xc, xoff + xgrp + xword_of<MMA>(p.BS, el[s].bl, el[s].d * GR + g), dry[g], step_tag(it));
+        }
+      }
     }
     prof.mark(3);
+    prof.stamp(it, 1);
 
     // ---- 2. dh_{t-1} partial = R^T dG_t over this wave's k-tiles, fused with the poll
     f32x4 acc[NB];
@@ -804,13 +851,14 @@ __global__ void __launch_bounds__(64 * (KSC + 1) * NDT) bwd_kernel(BwdArgs a) {
     auto prod = [&](int bt, int j, const Frag<MMA>& f) { acc[bt] = mma(A[j], f, acc[bt]); };
     uint32_t polls;
     if (NB == 1 && pair)
-      polls = gather_pair_mma<MMA, NF>(xc, xword_pair, bv_pair, xoff, nkt, step_tag(it), a.status, a.spin_limit,
+      polls = gather_pair_mma<MMA, NF>(xc, xword_pair, bv_pair, xoff, cstride, nkt, step_tag(it), a.status, a.spin_limit,
                                        abort, zero, prod);
     else
-      polls = gather_mma<MMA, NB, NF>(xc, xword, bval, xoff, nkt, step_tag(it), a.status, a.spin_limit, abort, zero,
+      polls = gather_mma<MMA, NB, NF>(xc, xword, bval, xoff, cstride, nkt, step_tag(it), a.status, a.spin_limit, abort, zero,
                                       prod);
     prof.add(4, polls);
     prof.mark(0);
+    prof.stamp(it, 2);
     float* rp = red + (long)(it & 1) * NB * 256 * KS;
 #pragma unroll
     for (int bt = 0; bt < NB; ++bt)
@@ -819,6 +867,7 @@ __global__ void __launch_bounds__(64 * (KSC + 1) * NDT) bwd_kernel(BwdArgs a) {
     prof.mark(1);
     __syncthreads();
     prof.mark(2);
+    prof.stamp(it, 3);
 
     // ---- 3. owners: reduce -> recurrent cotangent of h_{t-1}
 #pragma unroll
@@ -862,6 +911,7 @@ __global__ void __launch_bounds__(64 * (KSC + 1) * NDT) bwd_kernel(BwdArgs a) {
   }
   prof.acc[5] = T;
   prof.flush(a.prof ? a.prof + 128 : nullptr);
+  if (a.prof) prof.flush_trace(a.prof + 256 + 128 * 16 * 64);
 }
 
 }  // namespace frnn

@@ -127,7 +127,10 @@ int frnn_timing_read(double* ms3, int32_t* counts3);
  * [1] MFMA and LDS partials, [2] workgroup barrier, [3] cell arithmetic,
  * [4] exchange polls, [5] steps, [6] backward partial-sum reduction. I/O
  * waves: [0] ring fill, [1] load issue, [2] barrier, [3] output drain,
- * [5] steps. NULL disables. */
+ * [5] steps. Every wave of workgroups 0-127 also writes a timeline of steps
+ * 64-79 (four 100 MHz clock stamps per step, 64 words per wave) at word
+ * 256 + (workgroup * 16 + wave) * 64 (forward) and 131328 + the same
+ * (backward); the buffer then needs 262400 words. NULL disables. */
 void frnn_set_phase_profile(void* device_words);
 
 /* Test hook: the spin limit of the exchange waits (default 1<<22 polls; 0 restores it).
