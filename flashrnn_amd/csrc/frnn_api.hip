@@ -93,6 +93,27 @@ int ktw_class(int need, int ndt) {
   return 0;
 }
 
+// Whether a wave of a workgroup with `ks` compute waves per hidden tile holds
+// its resident R (forward) or R^T (backward) slice plus the exchange runs it
+// keeps in flight (at most 8 BF16 runs in one-tile workgroups, else 4) in its
+// share of the register file: the 512 registers of a SIMD lane divided among
+// the waves per SIMD, less 56 for the rest of the loop. The variant must also
+// be built.
+bool fits(const Plan& p, int ks, bool forward) {
+  const int need = (p.kt_fwd + ks - 1) / ks;
+  const int ktw = ktw_class(need, p.NDT);
+  if (!ktw || !frnn::recurrence_kernel(p.cell, p.mma, ks, ktw, p.NDT, forward)) return false;
+  if (p.NDT == 2 && ks != 3 && ks != 4) return false;
+  const int waves = p.NDT * (ks + 1);
+  const int per_simd = (waves + 3) / 4;
+  const int budget = (512 / per_simd) / 8 * 8 - 56;
+  const int frag = p.mma == FRNN_MMA_BF16 ? 4 : 8;  // registers of one resident fragment
+  const int run = 2 * frag;                         // registers of one in-flight exchange run
+  const int frags = p.GR * ktw;
+  const int runs = std::min(forward ? ktw : frags, (p.mma == FRNN_MMA_BF16 && p.NDT == 1) ? 8 : 4);
+  return frags * frag + runs * run <= budget;
+}
+
 // Groups [g0, g0 + n) form one launch; its grid in either placement mode.
 void set_groups(Plan* p, int g0, int n) {
   p->g0 = g0;
@@ -129,26 +150,24 @@ int make_plan(const frnn_desc* d, Plan* p) {
   p->NDT = (p->D / 16 <= 32) ? 1 : 2;
   // contraction split (compute waves per hidden tile, plus one I/O wave): forward
   // up to 4; backward up to 8 where D/32 >= 8 (its exchange operand is GR times
-  // wider, so splitting it further shortens each wave's poll). FRNN_KS /
-  // FRNN_KS_BWD (environment, read per plan) override within the built set.
+  // wider, so splitting it further shortens each wave's poll). Two-tile
+  // workgroups whose resident R slice does not fit beside 4 waves per tile use 3
+  // (8 waves: two per SIMD, 256 registers each). FRNN_KS / FRNN_KS_BWD
+  // (environment, read per plan) override within the built set.
   p->KS = KT >= 4 ? 4 : (KT >= 2 ? 2 : 1);
+  if (p->NDT == 2 && !fits(*p, 4, true)) p->KS = 3;
   p->KSB = (KT >= 8 && p->NDT == 1) ? 8 : p->KS;
+  if (p->NDT == 1 && p->KSB == 8 && !fits(*p, 8, false)) p->KSB = 4;
+  if (p->NDT == 2 && !fits(*p, p->KSB, false)) p->KSB = 3;
   auto ks_env = [&](const char* name, int* ks) {
     if (const char* e = std::getenv(name)) {
       const int v = std::atoi(e);
-      if ((v == 1 || v == 2 || v == 4 || (v == 8 && p->NDT == 1)) && v <= KT) *ks = v;
+      if ((v == 1 || v == 2 || v == 4 || (v == 8 && p->NDT == 1) || (v == 3 && p->NDT == 2)) && v <= KT) *ks = v;
     }
   };
   ks_env("FRNN_KS", &p->KS);
   ks_env("FRNN_KS_BWD", &p->KSB);
-  for (int ks : {p->KS, p->KSB}) {
-    const int need = (KT + ks - 1) / ks;
-    if (!ktw_class(need, p->NDT)) return FRNN_E_UNSUPPORTED;
-    // registers per lane held by the resident R^T and the dG fragments of the backward
-    const int frag_vgprs = p->mma == FRNN_MMA_BF16 ? 4 : 8;
-    const int vgpr_budget = p->NDT == 1 ? 200 : 112;
-    if (2 * p->GR * ktw_class(need, p->NDT) * frag_vgprs > vgpr_budget) return FRNN_E_UNSUPPORTED;
-  }
+  if (!fits(*p, p->KS, true) || !fits(*p, p->KSB, false)) return FRNN_E_UNSUPPORTED;
   p->epl = (4 * p->NB + p->KS - 1) / p->KS;
   p->nsave = nsave_of(p->cell);
   p->wpg = p->D / (16 * p->NDT);

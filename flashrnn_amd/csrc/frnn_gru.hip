@@ -1,8 +1,8 @@
 // Recurrence kernels of the gru cell: every built (operand type, contraction
 // split, k-tiles per wave, hidden tiles per workgroup) variant. The planner
-// picks KS = min(4, largest power of two <= D/32), or 8 on request; one-tile workgroups
-// (widths up to 512) use k-tile classes 1, 2, 4; two-tile workgroups
-// (widths above 512) use classes 6 and 8 with KS = 4.
+// picks KS = min(4, largest power of two <= D/32), 8 for the backward where
+// D/32 >= 8; one-tile workgroups (widths up to 512) use k-tile classes 1, 2, 4;
+// two-tile workgroups (widths 544-768) use classes 6 and 8 with KS = 3, BF16 only.
 #include "frnn_kernels.h"
 #include "frnn_recurrence.h"
 
@@ -24,8 +24,10 @@ static const void* by_shape(int ks, int ktw, int ndt, bool fwd) {
   if (ndt == 1 && ks == 4 && ktw == 4) return pick<MMA, 4, 1, 4>(fwd);
   if (ndt == 1 && ks == 8 && ktw == 1) return pick<MMA, 1, 1, 8>(fwd);
   if (ndt == 1 && ks == 8 && ktw == 2) return pick<MMA, 2, 1, 8>(fwd);
-  if (ndt == 2 && ks == 4 && ktw == 6) return pick<MMA, 6, 2, 4>(fwd);
-  if (ndt == 2 && ks == 4 && ktw == 8) return pick<MMA, 8, 2, 4>(fwd);
+  if constexpr (MMA == MMA_BF16) {  // two-tile workgroups: only the BF16 slice fits beside the runs
+    if (ndt == 2 && ks == 3 && ktw == 6) return pick<MMA, 6, 2, 3>(fwd);
+    if (ndt == 2 && ks == 3 && ktw == 8) return pick<MMA, 8, 2, 3>(fwd);
+  }
   return nullptr;
 }
 

@@ -30,18 +30,22 @@
 
 namespace frnn {
 
-constexpr int kFwdRing = 4;  // Wx steps staged ahead
+constexpr int kFwdRing = 4;   // Wx ring slots in LDS
+constexpr int kFwdAhead = 3;  // steps of Wx in flight: one less than the slots, so a
+                              // load never lands in the slot the owners are reading
 
 template <int CELL>
 struct BwdRing {  // input steps staged ahead, bounded by the I/O wave's registers
   static constexpr int P = 2;
 };
 
-// LDS layout of a team. Everything an owner lane needs for one element is
-// contiguous, so it arrives in a few 16-byte reads issued together:
+// LDS layout of a team:
 //   forward : red  [2][KS][NB][64 lanes][4 regs][4 gates]  MFMA partial sums
-//             xring[P][NE][GWP]                           Wx of the next steps
-//             ost  [2][NE][NOP]                           states + saved values
+//             xring[slot][gate][64 chunks][16 bytes]       raw Wx of the next steps
+//                  (chunk = row * 4 + quad: FP32 units 4*quad..+3; BF16 units
+//                   4*quad..+7 in the even quads, odd quads unused)
+//             ost  [2][value][NE]                         states + saved values,
+//                  value-major so the drain reads 4 elements per 16-byte read
 //   backward: red  [2][NB][64 lanes][4 regs][KS]          partial R^T dG
 //             iring[P][NE][NOP]                           state cotangents + saved values
 //             ost  [2][NE][4]                             dWx (+ GRU candidate cotangent)
@@ -50,12 +54,13 @@ struct Lds {
   static constexpr int NE = NB * 256;
   static constexpr int GR = CellShape<CELL>::GR, GW = CellShape<CELL>::GW, S = CellShape<CELL>::S;
   static constexpr int NSAVE = Cell<CELL>::NSAVE;
-  static constexpr int GWP = GW == 1 ? 1 : 4;                // Wx gates per element, padded
   static constexpr int NOP = (S + NSAVE + 3) / 4 * 4;        // per-element staged values, padded
   static constexpr int NOB = 4;                              // backward outputs per element, padded
   // floats per team
+  static constexpr int NV = S + NSAVE;                      // staged values per element (forward)
+  static constexpr int RING = GW * 64 * 4;                   // floats per Wx ring slot
   __host__ __device__ static constexpr long fwd(int KS) {
-    return 2L * KS * NB * 1024 + (long)kFwdRing * NE * GWP + 2L * NE * NOP;
+    return 2L * KS * NB * 1024 + (long)kFwdRing * RING + 2L * NV * NE;
   }
   __host__ __device__ static constexpr long bwd(int KS) {
     return 2L * NB * 256 * KS + (long)BwdRing<CELL>::P * NE * NOP + 2L * NE * NOB;
@@ -162,6 +167,14 @@ struct Prof {
   }
 };
 
+// Runs a wave keeps in flight at most (8 BF16 runs or 4 FP32 runs: 64
+// registers; 4 runs in two-tile workgroups, whose resident slice is larger);
+// a longer contraction range is polled chunk by chunk, which bounds the
+// registers of the in-flight loads.
+template <int MMA, int NDT> struct PollChunk {
+  static constexpr int value = (MMA == MMA_BF16 && NDT == 1) ? 8 : 4;
+};
+
 // Poll the exchange and run the step's product on it, fused. Every 8-word run
 // of this wave's contraction range is loaded at once; as each arrives it is
 // unpacked, its tags checked, and its MFMAs issued into the caller's
@@ -169,43 +182,96 @@ struct Prof {
 // stale the accumulators are cleared and the poll repeats. Runs of padded batch
 // rows are not read (they contribute zero). zero() clears the accumulators,
 // prod(bt, j, frag) adds run j of batch tile bt. Returns the number of polls.
-template <int MMA, int NB, int NF, typename Zero, typename Prod>
+//
+// Ranges of more than PollChunk runs are polled in chunks: each chunk is
+// polled until all of its tags are fresh and only then multiplied, so a
+// stale chunk never has to be taken back out of the accumulators.
+template <int MMA, int NDT, int NB, int NF, typename Zero, typename Prod>
 __device__ __forceinline__ uint32_t gather_mma(const Xchg& x, const int (&word)[NB][NF], const bool (&bval)[NB],
                                                int off, int cstride, int nf, uint32_t tag, uint32_t* status, uint32_t spin_limit,
                                                bool& abort, Zero zero, Prod prod) {
   uint32_t spins = 0;
-  while (true) {
-    zero();
-    if (abort) return spins;
-    Run<MMA> r[NB][NF];
+  if constexpr (NF <= PollChunk<MMA, NDT>::value) {
+    while (true) {
+      zero();
+      if (abort) return spins;
+      Run<MMA> r[NB][NF];
 #pragma unroll
-    for (int bt = 0; bt < NB; ++bt)
+      for (int bt = 0; bt < NB; ++bt)
 #pragma unroll
-      for (int j = 0; j < NF; ++j) {
-        r[bt][j].zero();
-        if (j < nf && bval[bt]) xload<MMA>(x, word[bt][j] + off, cstride, r[bt][j]);
-      }
-    // Branch-free from here on: the MFMAs read operands across lanes and must
-    // run with the whole wave active, so lane-dependent conditions are selects.
-    bool ok = true;
-#pragma unroll
-    for (int bt = 0; bt < NB; ++bt)
-#pragma unroll
-      for (int j = 0; j < NF; ++j)
-        if (j < nf) {
-          Frag<MMA> f;
-          const bool fresh = xunpack<MMA>(r[bt][j], tag, f);
-          ok &= fresh || !bval[bt];
-          prod(bt, j, frag_keep<MMA>(bval[bt], f));
+        for (int j = 0; j < NF; ++j) {
+          r[bt][j].zero();
+          if (j < nf && bval[bt]) xload<MMA>(x, word[bt][j] + off, cstride, r[bt][j]);
         }
-    ++spins;
-    if (__all(ok)) return spins;
-    if (spins >= spin_limit) {
-      raise_status(status, ST_TIMEOUT);
-      abort = true;
-    } else if ((spins & 63u) == 0 && load_status(status) != 0) {
-      abort = true;
+      // Branch-free from here on: the MFMAs read operands across lanes and must
+      // run with the whole wave active, so lane-dependent conditions are selects.
+      bool ok = true;
+#pragma unroll
+      for (int bt = 0; bt < NB; ++bt)
+#pragma unroll
+        for (int j = 0; j < NF; ++j)
+          if (j < nf) {
+            Frag<MMA> f;
+            const bool fresh = xunpack<MMA>(r[bt][j], tag, f);
+            ok &= fresh || !bval[bt];
+            prod(bt, j, frag_keep<MMA>(bval[bt], f));
+          }
+      ++spins;
+      if (__all(ok)) return spins;
+      if (spins >= spin_limit) {
+        raise_status(status, ST_TIMEOUT);
+        abort = true;
+      } else if ((spins & 63u) == 0 && load_status(status) != 0) {
+        abort = true;
+      }
     }
+  } else {
+    constexpr int CH = PollChunk<MMA, NDT>::value;
+    zero();
+#pragma unroll
+    for (int c0 = 0; c0 < NF; c0 += CH) {
+      if (c0 >= nf) break;
+      while (true) {
+        if (abort) return spins;
+        Run<MMA> r[NB][CH];
+#pragma unroll
+        for (int bt = 0; bt < NB; ++bt)
+#pragma unroll
+          for (int jj = 0; jj < CH; ++jj) {
+            r[bt][jj].zero();
+            if (c0 + jj < NF && c0 + jj < nf && bval[bt]) xload<MMA>(x, word[bt][c0 + jj < NF ? c0 + jj : 0] + off, cstride, r[bt][jj]);
+          }
+        bool ok = true;
+#pragma unroll
+        for (int bt = 0; bt < NB; ++bt)
+#pragma unroll
+          for (int jj = 0; jj < CH; ++jj)
+            if (c0 + jj < NF && c0 + jj < nf) {
+              Frag<MMA> f;
+              ok &= xunpack<MMA>(r[bt][jj], tag, f) || !bval[bt];
+            }
+        ++spins;
+        if (__all(ok)) {
+#pragma unroll
+          for (int bt = 0; bt < NB; ++bt)
+#pragma unroll
+            for (int jj = 0; jj < CH; ++jj)
+              if (c0 + jj < NF && c0 + jj < nf) {
+                Frag<MMA> f;
+                xunpack<MMA>(r[bt][jj], tag, f);
+                prod(bt, c0 + jj, frag_keep<MMA>(bval[bt], f));
+              }
+          break;
+        }
+        if (spins >= spin_limit) {
+          raise_status(status, ST_TIMEOUT);
+          abort = true;
+        } else if ((spins & 63u) == 0 && load_status(status) != 0) {
+          abort = true;
+        }
+      }
+    }
+    return spins;
   }
 }
 
@@ -214,45 +280,83 @@ __device__ __forceinline__ uint32_t gather_mma(const Xchg& x, const int (&word)[
 // polls the odd k-tile of each pair for the same batch row, so a lane issues
 // half the loads; the odd tile then moves down 8 lanes (DPP) and the upper
 // lanes contribute zero. word[j] is the run of k-tile j for batch row lane % 8.
-template <int MMA, int NF, typename Zero, typename Prod>
+// Long ranges are polled in chunks of PollChunk pairs, as in gather_mma.
+template <int MMA, int NDT, int NF, typename Zero, typename Prod>
 __device__ __forceinline__ uint32_t gather_pair_mma(const Xchg& x, const int (&word)[NF], bool bv, int off, int cstride, int nf,
                                                     uint32_t tag, uint32_t* status, uint32_t spin_limit, bool& abort,
                                                     Zero zero, Prod prod) {
   constexpr int NP = (NF + 1) / 2;
+  constexpr int CH = NP <= PollChunk<MMA, NDT>::value ? NP : PollChunk<MMA, NDT>::value;
   const int hi = (threadIdx.x >> 3) & 1;  // lane % 16 >= 8
   uint32_t spins = 0;
-  while (true) {
-    zero();
-    if (abort) return spins;
-    Run<MMA> r[NP];
+  zero();
 #pragma unroll
-    for (int i = 0; i < NP; ++i) {
-      r[i].zero();
-      if (2 * i + hi < nf && bv) xload<MMA>(x, word[2 * i + hi] + off, cstride, r[i]);
-    }
-    // Branch-free from here on (cross-lane DPP and MFMA need the whole wave).
-    bool ok = true;
+  for (int i0 = 0; i0 < NP; i0 += CH) {
+    if (2 * i0 >= nf) break;
+    while (true) {
+      if constexpr (NP <= PollChunk<MMA, NDT>::value) zero();
+      if (abort) return spins;
+      Run<MMA> r[CH];
 #pragma unroll
-    for (int i = 0; i < NP; ++i) {
-      if (2 * i >= nf) continue;
-      const bool v = 2 * i + hi < nf && bv;
-      Frag<MMA> f;
-      const bool fresh = xunpack<MMA>(r[i], tag, f);
-      ok &= fresh || !v;
-      f = frag_keep<MMA>(v, f);
-      const Frag<MMA> odd = frag_rot8(f);
-      prod(0, 2 * i, frag_keep<MMA>(!hi, f));
-      if (2 * i + 1 < nf) prod(0, 2 * i + 1, frag_keep<MMA>(!hi, odd));
-    }
-    ++spins;
-    if (__all(ok)) return spins;
-    if (spins >= spin_limit) {
-      raise_status(status, ST_TIMEOUT);
-      abort = true;
-    } else if ((spins & 63u) == 0 && load_status(status) != 0) {
-      abort = true;
+      for (int ii = 0; ii < CH; ++ii) {
+        const int i = i0 + ii;
+        r[ii].zero();
+        if (i < NP && 2 * i + hi < nf && bv) xload<MMA>(x, word[i < NP ? 2 * i + hi : 0] + off, cstride, r[ii]);
+      }
+      // Branch-free from here on (cross-lane DPP and MFMA need the whole wave).
+      bool ok = true;
+      if constexpr (NP <= PollChunk<MMA, NDT>::value) {
+        // one chunk: multiply speculatively while the tags are checked
+#pragma unroll
+        for (int ii = 0; ii < CH; ++ii) {
+          const int i = i0 + ii;
+          if (2 * i >= nf) continue;
+          const bool v = 2 * i + hi < nf && bv;
+          Frag<MMA> f;
+          const bool fresh = xunpack<MMA>(r[ii], tag, f);
+          ok &= fresh || !v;
+          f = frag_keep<MMA>(v, f);
+          const Frag<MMA> odd = frag_rot8(f);
+          prod(0, 2 * i, frag_keep<MMA>(!hi, f));
+          if (2 * i + 1 < nf) prod(0, 2 * i + 1, frag_keep<MMA>(!hi, odd));
+        }
+      } else {
+#pragma unroll
+        for (int ii = 0; ii < CH; ++ii) {
+          const int i = i0 + ii;
+          if (i >= NP || 2 * i >= nf) continue;
+          const bool v = 2 * i + hi < nf && bv;
+          Frag<MMA> f;
+          ok &= xunpack<MMA>(r[ii], tag, f) || !v;
+        }
+      }
+      ++spins;
+      if (__all(ok)) {
+        if constexpr (NP > PollChunk<MMA, NDT>::value) {
+#pragma unroll
+          for (int ii = 0; ii < CH; ++ii) {
+            const int i = i0 + ii;
+            if (i >= NP || 2 * i >= nf) continue;
+            const bool v = 2 * i + hi < nf && bv;
+            Frag<MMA> f;
+            xunpack<MMA>(r[ii], tag, f);
+            f = frag_keep<MMA>(v, f);
+            const Frag<MMA> odd = frag_rot8(f);
+            prod(0, 2 * i, frag_keep<MMA>(!hi, f));
+            if (2 * i + 1 < nf) prod(0, 2 * i + 1, frag_keep<MMA>(!hi, odd));
+          }
+        }
+        break;
+      }
+      if (spins >= spin_limit) {
+        raise_status(status, ST_TIMEOUT);
+        abort = true;
+      } else if ((spins & 63u) == 0 && load_status(status) != 0) {
+        abort = true;
+      }
     }
   }
+  return spins;
 }
 
 // ====================================================================== forward
@@ -261,98 +365,104 @@ __device__ __forceinline__ uint32_t gather_pair_mma(const Xchg& x, const int (&w
 // vector access and every LDS access one 16-byte access.
 __device__ __forceinline__ int io_elem(int lane, int i) { return 256 * (i >> 2) + 4 * lane + (i & 3); }
 
-// I/O wave of a team: Wx of step t+P into the ring, outputs of step t-1 to HBM.
+// s_waitcnt that waits until at most n vector-memory operations of this wave
+// are outstanding (gfx9 encoding: vmcnt in bits 3:0 and 15:14; expcnt and
+// lgkmcnt left at their maxima, i.e. not waited for).
+template <int n>
+__device__ __forceinline__ void wait_vm() {
+  static_assert(n >= 0 && n < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// Wx value of gate g for owned element (slab row r, unit d of the tile) from
+// a raw ring slot (see the LDS layout above).
+__device__ __forceinline__ float ring_x(const float* slot, int g, int r, int d, int dt) {
+  if (dt == DT_F32) return slot[(g * 64 + r * 4 + (d >> 2)) * 4 + (d & 3)];
+  const unsigned short* h = reinterpret_cast<const unsigned short*>(slot);
+  return bf16_to_f32(h[(g * 64 + r * 4 + (d >> 3) * 2) * 8 + (d & 7)]);
+}
+
+// I/O wave of a team. Wx of step u is loaded straight into ring slot
+// u % kFwdRing by LDS-DMA (global_load_lds: no registers in flight), issued
+// kFwdAhead steps ahead; before barrier t the wave waits, by count, until the
+// loads of step t+1 have landed, so the owners read step t+1's Wx right after
+// their step-t cell, off the critical path. After barrier t it drains the
+// outputs of step t-1, then issues the loads of step t+kFwdAhead. Per step the
+// wave issues the same stores and loads in the same order, so the count of
+// operations issued after a step's loads is a constant in the steady state
+// (the first and last steps wait for everything). Padding batch rows are
+// neither loaded nor stored.
 template <int CELL, int MMA, int NB>
 __device__ void fwd_io(const FwdArgs& a, const Team& tm, float* xring, float* ost) {
+  static_assert(NB == 1, "one 16-row batch tile per group");
   using CS = CellShape<CELL>;
-  constexpr int GW = CS::GW, S = CS::S, NE = NB * 256, IOQ = NB, P = kFwdRing;  // IOQ quads per lane
-  constexpr int NSAVE = Cell<CELL>::NSAVE, NOP = Lds<CELL, NB>::NOP, GWP = Lds<CELL, NB>::GWP;
+  constexpr int GW = CS::GW, S = CS::S, NE = NB * 256, P = kFwdAhead;
+  constexpr int NSAVE = Cell<CELL>::NSAVE, NV = Lds<CELL, NB>::NV, RING = Lds<CELL, NB>::RING;
   const Plan& p = a.p;
   const int T = p.T, N = p.N, D = p.D, B = p.B;
   const bool training = (p.flags & 1) != 0;
   const long wx_t = (long)GW * N * D;
-  Elem el[IOQ];
-  int e0[IOQ];
+  // loads: lane -> (row, quad); BF16 chunks hold 8 units, so odd quads idle
+  const int lrow = tm.lane >> 2, lquad = tm.lane & 3;
+  const int lb = tm.slab * p.BS + lrow;
+  const bool lval = lb < B && (p.dt_io == DT_F32 || (lquad & 1) == 0);
+  const long lbase = ((long)lb * T) * wx_t + (long)tm.n * D + tm.dt * 16 + 4 * lquad;
+  const int esz = p.dt_io == DT_F32 ? 4 : 2;
+  auto load_wx = [&](int u) {
+    float* slot = xring + (long)(u % kFwdRing) * RING;
 #pragma unroll
-  for (int q = 0; q < IOQ; ++q) {
-    e0[q] = io_elem(tm.lane, 4 * q);
-    el[q] = elem_of(p, tm, e0[q]);
-  }
-  auto load_wx = [&](int t, u32x4 (&dst)[IOQ][GW]) {
-#pragma unroll
-    for (int q = 0; q < IOQ; ++q)
-#pragma unroll
-      for (int g = 0; g < GW; ++g)
-        dst[q][g] = el[q].real
-                        ? ld4_raw(a.wx, ((long)el[q].b * T + t) * wx_t + ((long)g * N + tm.n) * D + el[q].d, p.dt_io)
-                        : u32x4{0u, 0u, 0u, 0u};
-  };
-  auto store_out = [&](int t, const float* src) {
-#pragma unroll
-    for (int q = 0; q < IOQ; ++q) {
-      const int e = e0[q];
-      // the quad's staged vectors, transposed to one f32x4 (4 elements) per value
-      f32x4 in[4][NOP / 4];
-#pragma unroll
-      for (int k = 0; k < 4; ++k)
-#pragma unroll
-        for (int c = 0; c < NOP / 4; ++c) in[k][c] = *reinterpret_cast<const f32x4*>(src + (e + k) * NOP + 4 * c);
-      auto val = [&](int v) { return f32x4{in[0][v / 4][v % 4], in[1][v / 4][v % 4], in[2][v / 4][v % 4], in[3][v / 4][v % 4]}; };
-      if (el[q].real)
-#pragma unroll
-        for (int k = 0; k < S; ++k)
-          st4(a.states, ((((long)k * B + el[q].b) * T + t) * N + tm.n) * D + el[q].d, p.dt_io, val(k));
-      if (training)
-#pragma unroll
-        for (int v = 0; v < NSAVE; ++v)
-          *reinterpret_cast<f32x4*>(a.save + save_index(p, NE, t, tm.wgi, v, tm.team, e)) = val(S + v);
+    for (int g = 0; g < GW; ++g) {
+      const char* src = static_cast<const char*>(a.wx) + (lbase + (long)u * wx_t + (long)g * N * D) * esz;
+      if (lval)
+        __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)(slot + g * 256), 16, 0, 0);
     }
   };
+  // stores: lane -> elements e0 .. e0+3 (four units of one row)
+  const int e0 = io_elem(tm.lane, 0);
+  const Elem el = elem_of(p, tm, e0);
+  auto store_out = [&](int t, const float* src) {
+#pragma unroll
+    for (int v = 0; v < NV; ++v) {
+      if (v >= S && !training) break;
+      const f32x4 x = *reinterpret_cast<const f32x4*>(src + v * NE + e0);
+      if (!el.real) continue;
+      if (v < S)
+        st4(a.states, ((((long)v * B + el.b) * T + t) * N + tm.n) * D + el.d, p.dt_io, x);
+      else
+        *reinterpret_cast<f32x4*>(a.save + save_index(p, NE, t, tm.wgi, v - S, tm.team, e0)) = x;
+    }
+  };
+  // VMEM operations issued after the loads of step t+1, at the top of
+  // iteration t (steady state): P-2 iterations of stores and loads
+  static_assert(P >= 2, "prefetch distance");
+  constexpr int kAfterTrain = (P - 2) * (GW + NV), kAfterInfer = (P - 2) * (GW + S);
 
   Prof prof;
   prof.init(a.prof != nullptr && blockIdx.x == 0, a.prof != nullptr);
-  u32x4 buf[P][IOQ][GW];
-#pragma unroll
-  for (int j = 0; j < P; ++j)
-    if (j < T) load_wx(j, buf[j]);
-  for (int t0 = 0; t0 < T; t0 += P) {
-#pragma unroll
-    for (int j = 0; j < P; ++j) {
-      const int t = t0 + j;
-      if (t < T) {
-#pragma unroll
-        for (int q = 0; q < IOQ; ++q) {
-          f32x4 x[GW];
-#pragma unroll
-          for (int g = 0; g < GW; ++g) x[g] = raw4_f32(buf[j][q][g], p.dt_io);
-          if constexpr (GWP == 1) {
-            *reinterpret_cast<f32x4*>(xring + (long)j * NE + e0[q]) = x[0];
-          } else {
-#pragma unroll
-            for (int k = 0; k < 4; ++k) {
-              f32x4 v = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-              for (int g = 0; g < GW; ++g) v[g] = x[g][k];
-              *reinterpret_cast<f32x4*>(xring + ((long)j * NE + e0[q] + k) * GWP) = v;
-            }
-          }
-        }
-        prof.mark(0);
-        prof.stamp(t, 0);
-        if (t + P < T) load_wx(t + P, buf[j]);
-        prof.mark(1);
-        prof.stamp(t, 1);
-        __syncthreads();  // step t: Wx_t staged; outputs of step t-1 complete
-        prof.mark(2);
-        prof.stamp(t, 2);
-        if (t >= 1) store_out(t - 1, ost + ((t - 1) & 1) * NOP * NE);
-        prof.mark(3);
-        prof.stamp(t, 3);
-      }
+  for (int u = 0; u < P && u < T; ++u) load_wx(u);
+  wait_vm<0>();
+  __syncthreads();  // Wx_0 in its slot
+  for (int t = 0; t < T; ++t) {
+    if (t + 1 >= P && t + P <= T) {
+      if (training) wait_vm<kAfterTrain>();
+      else wait_vm<kAfterInfer>();
+    } else {
+      wait_vm<0>();
     }
+    prof.mark(0);
+    prof.stamp(t, 0);
+    prof.mark(1);
+    prof.stamp(t, 1);
+    __syncthreads();  // step t: Wx_{t+1} in its slot; outputs of step t-1 staged
+    prof.mark(2);
+    prof.stamp(t, 2);
+    if (t >= 1) store_out(t - 1, ost + ((t - 1) & 1) * NV * NE);
+    if (t + P < T) load_wx(t + P);
+    prof.mark(3);
+    prof.stamp(t, 3);
   }
   __syncthreads();  // outputs of the last step complete
-  store_out(T - 1, ost + ((T - 1) & 1) * NOP * NE);
+  store_out(T - 1, ost + ((T - 1) & 1) * NV * NE);
   prof.acc[5] = T;
   prof.flush(a.prof);
   if (a.prof) prof.flush_trace(a.prof + 256);
@@ -363,7 +473,7 @@ __global__ void __launch_bounds__(64 * (KSC + 1) * NDT) fwd_kernel(FwdArgs a) {
   using CS = CellShape<CELL>;
   constexpr int GR = CS::GR, GW = CS::GW, GT = CS::GT, S = CS::S;
   constexpr int NE = NB * 256, EPLMAX = (4 * NB + KSC - 1) / KSC, KS = KSC;
-  constexpr int NSAVE = Cell<CELL>::NSAVE, NOP = Lds<CELL, NB>::NOP, GWP = Lds<CELL, NB>::GWP;
+  constexpr int NSAVE = Cell<CELL>::NSAVE, NV = Lds<CELL, NB>::NV, RING = Lds<CELL, NB>::RING;
   const Plan& p = a.p;
   Team tm;
   if (!team_setup(p, tm, a.status, KSC)) return;
@@ -371,8 +481,8 @@ __global__ void __launch_bounds__(64 * (KSC + 1) * NDT) fwd_kernel(FwdArgs a) {
 
   extern __shared__ float lds[];
   float* red = lds + tm.team * Lds<CELL, NB>::fwd(KS);  // [2][KS][NB][64][4][4]
-  float* xring = red + 2L * KS * NB * 1024;             // [P][NE][GWP]
-  float* ost = xring + (long)kFwdRing * NE * GWP;       // [2][NE][NOP]
+  float* xring = red + 2L * KS * NB * 1024;             // [slot][gate][64][4]
+  float* ost = xring + (long)kFwdRing * RING;           // [2][NV][NE]
 
   // sLSTM: the reference's global predicate all(n0 == 0) over the call's whole initial state
   uint32_t zflag = 0;
@@ -449,12 +559,29 @@ __global__ void __launch_bounds__(64 * (KSC + 1) * NDT) fwd_kernel(FwdArgs a) {
     for (int g = 0; g < GT; ++g) bias[s][g] = own[s] ? ld_val(a.bias, ((long)g * N + tm.n) * D + el[s].d, p.dt_io) : 0.f;
   }
 
+  // The initial hidden state goes through the exchange like any other step's:
+  // step 0 polls the parity and tag of step -1.
+#pragma unroll
+  for (int s = 0; s < EPLMAX; ++s)
+    if (el[s].real) xstore<MMA>(xc, xpar + xgrp + xword_of<MMA>(p.BS, el[s].bl, el[s].d), st[s][0], step_tag(-1));
+
   Prof prof;
   prof.init(a.prof != nullptr && blockIdx.x == 0, a.prof != nullptr);
   // Retire every set-up load before the loop: the wait-count pass then sees no
   // load still pending at the loop head, and does not fence the exchange
   // stores inside the loop behind one.
   __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();  // Wx_0 in its slot
+  // Wx of the next step, read from the ring right after each cell
+  float xnext[EPLMAX][GW];
+  auto read_x = [&](int u) {
+    const float* xr = xring + (long)(u % kFwdRing) * RING;
+#pragma unroll
+    for (int s = 0; s < EPLMAX; ++s)
+#pragma unroll
+      for (int g = 0; g < GW; ++g) xnext[s][g] = el[s].real ? ring_x(xr, g, el[s].bl, el[s].d & 15, p.dt_io) : 0.f;
+  };
+  read_x(0);
   bool abort = false;
   for (int t = 0; t < T; ++t) {
     prof.stamp(t, 0);
@@ -470,31 +597,14 @@ __global__ void __launch_bounds__(64 * (KSC + 1) * NDT) fwd_kernel(FwdArgs a) {
 #pragma unroll
       for (int g = 0; g < GR; ++g) acc[bt][g] = mma(A[g][j], f, acc[bt][g]);
     };
-    if (t == 0) {
-      zero();
-#pragma unroll
-      for (int bt = 0; bt < NB; ++bt)
-#pragma unroll
-        for (int j = 0; j < KTW; ++j)
-          if (j < nkt) {
-            Frag<MMA> f;
-            f.zero();
-            if (bval[bt]) {
-              const int b = tm.slab * p.BS + bt * 16 + tm.row;
-              const long base = ((long)b * N + tm.n) * D + (kt0 + j) * 32 + 8 * tm.kq;
-#pragma unroll
-              for (int i = 0; i < 8; ++i) frag_set(f, i, ld_val(a.s0, base + i, p.dt_state));
-            }
-            prod(bt, j, f);
-          }
-    } else {
+    {
       uint32_t polls;
       const int off = ((t - 1) & 1) * xpar;
       if (NB == 1 && pair)
-        polls = gather_pair_mma<MMA, KTW>(xc, xword_pair, bv_pair, off, cstride, nkt, step_tag(t - 1), a.status, a.spin_limit,
+        polls = gather_pair_mma<MMA, NDT, KTW>(xc, xword_pair, bv_pair, off, cstride, nkt, step_tag(t - 1), a.status, a.spin_limit,
                                           abort, zero, prod);
       else
-        polls = gather_mma<MMA, NB, KTW>(xc, xword, bval, off, cstride, nkt, step_tag(t - 1), a.status, a.spin_limit, abort,
+        polls = gather_mma<MMA, NDT, NB, KTW>(xc, xword, bval, off, cstride, nkt, step_tag(t - 1), a.status, a.spin_limit, abort,
                                          zero, prod);
       prof.add(4, polls);
     }
@@ -516,8 +626,7 @@ __global__ void __launch_bounds__(64 * (KSC + 1) * NDT) fwd_kernel(FwdArgs a) {
     prof.stamp(t, 2);
 
     // ---- 3. owners: gates, cell, staged outputs, exchange
-    const float* xr = xring + (long)(t % kFwdRing) * NE * GWP;
-    float* os = ost + (long)(t & 1) * NE * NOP;
+    float* os = ost + (long)(t & 1) * NV * NE;
 #pragma unroll
     for (int s = 0; s < EPLMAX; ++s) {
       if (!own[s]) continue;
@@ -527,13 +636,8 @@ __global__ void __launch_bounds__(64 * (KSC + 1) * NDT) fwd_kernel(FwdArgs a) {
 #pragma unroll
       for (int w2 = 0; w2 < KS; ++w2) part[w2] = *reinterpret_cast<const f32x4*>(rp + w2 * NB * 1024 + src);
       float xcur[GW];
-      if constexpr (GWP == 1) {
-        xcur[0] = xr[e];
-      } else {
-        const f32x4 xv = *reinterpret_cast<const f32x4*>(xr + e * GWP);
 #pragma unroll
-        for (int g = 0; g < GW; ++g) xcur[g] = xv[g];
-      }
+      for (int g = 0; g < GW; ++g) xcur[g] = xnext[s][g];
       float ry[GR];
 #pragma unroll
       for (int g = 0; g < GR; ++g) {
@@ -551,23 +655,17 @@ __global__ void __launch_bounds__(64 * (KSC + 1) * NDT) fwd_kernel(FwdArgs a) {
         for (int g = 0; g < GR; ++g) g4[g] = xcur[g] + ry[g] + bias[s][g];
         Cell<CELL>::fwd(g4, st[s], sv, (CELL == CELL_SLSTM && t == 0) ? zflag : 0u);
       }
-      float outv[NOP];
-#pragma unroll
-      for (int k = 0; k < S; ++k) outv[k] = st[s][k];
-#pragma unroll
-      for (int v = 0; v < NSAVE; ++v) outv[S + v] = sv[v];
-#pragma unroll
-      for (int v = S + NSAVE; v < NOP; ++v) outv[v] = 0.f;
-#pragma unroll
-      for (int c = 0; c < NOP / 4; ++c)
-        *reinterpret_cast<f32x4*>(os + e * NOP + 4 * c) = f32x4{outv[4 * c], outv[4 * c + 1], outv[4 * c + 2], outv[4 * c + 3]};
-      // the exchange word goes out last: nothing after it in this step waits for its completion
+      // the exchange word goes out first: it is what the other workgroups wait for
       if (el[s].real && t + 1 < T)
         xstore<MMA>(xc, (t & 1) * xpar + xgrp + xword_of<MMA>(p.BS, el[s].bl, el[s].d), st[s][0], step_tag(t));
+#pragma unroll
+      for (int k = 0; k < S; ++k) os[k * NE + e] = st[s][k];
+#pragma unroll
+      for (int v = 0; v < NSAVE; ++v) os[(S + v) * NE + e] = sv[v];
     }
+    if (t + 1 < T) read_x(t + 1);  // landed before barrier t
     prof.mark(3);
     prof.stamp(t, 3);
-
   }
   __syncthreads();  // the I/O wave drains the last step
 
@@ -614,7 +712,9 @@ __device__ void bwd_io(const BwdArgs& a, const Team& tm, float* iring, float* os
                         : u32x4{0u, 0u, 0u, 0u};
 #pragma unroll
       for (int v = 0; v < NSAVE; ++v)
-        dst[q][S + v] = *reinterpret_cast<const u32x4*>(a.save + save_index(p, NE, t, tm.wgi, v, tm.team, e0[q]));
+        dst[q][S + v] = el[q].real  // padding rows were not saved
+                            ? *reinterpret_cast<const u32x4*>(a.save + save_index(p, NE, t, tm.wgi, v, tm.team, e0[q]))
+                            : u32x4{0u, 0u, 0u, 0u};
     }
   };
   auto stage = [&](int slot, const u32x4 (&src)[IOQ][NIN]) {
@@ -851,10 +951,10 @@ __global__ void __launch_bounds__(64 * (KSC + 1) * NDT) bwd_kernel(BwdArgs a) {
     auto prod = [&](int bt, int j, const Frag<MMA>& f) { acc[bt] = mma(A[j], f, acc[bt]); };
     uint32_t polls;
     if (NB == 1 && pair)
-      polls = gather_pair_mma<MMA, NF>(xc, xword_pair, bv_pair, xoff, cstride, nkt, step_tag(it), a.status, a.spin_limit,
+      polls = gather_pair_mma<MMA, NDT, NF>(xc, xword_pair, bv_pair, xoff, cstride, nkt, step_tag(it), a.status, a.spin_limit,
                                        abort, zero, prod);
     else
-      polls = gather_mma<MMA, NB, NF>(xc, xword, bval, xoff, cstride, nkt, step_tag(it), a.status, a.spin_limit, abort, zero,
+      polls = gather_mma<MMA, NDT, NB, NF>(xc, xword, bval, xoff, cstride, nkt, step_tag(it), a.status, a.spin_limit, abort, zero,
                                       prod);
     prof.add(4, polls);
     prof.mark(0);

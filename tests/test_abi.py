@@ -88,6 +88,22 @@ def test_unsupported_widths(lib, D):
     assert lib.frnn_fwd(ctypes.byref(d), *([None] * 8), 0, None) == -2
 
 
+@pytest.mark.parametrize(
+    "cell,D,mma,ok",
+    [
+        ("lstm", 512, "bf16", True), ("gru", 768, "bf16", True), ("lstm", 768, "bf16", True),
+        ("slstm", 576, "bf16", True), ("elman", 1024, "bf16", True), ("gru", 800, "bf16", False),
+        ("lstm", 1024, "bf16", False), ("lstm", 512, "f32", True), ("gru", 768, "f32", False),
+        ("elman", 768, "f32", True),
+    ],
+)
+def test_width_support(lib, cell, D, mma, ok):
+    """The plan's register budget: which head widths each operand type supports."""
+    m = _lib.FRNN_MMA_BF16 if mma == "bf16" else _lib.FRNN_MMA_F32
+    d = desc(cell=cell, B=16, T=8, N=1, D=D, mma=m)
+    assert (lib.frnn_workspace_bytes(ctypes.byref(d), 0) > 0) == ok
+
+
 def test_null_pointers_rejected_before_launch(lib):
     d = desc(B=2, T=4, N=1, D=64)
     assert lib.frnn_fwd(ctypes.byref(d), *([None] * 8), 0, None) == -1

@@ -1,6 +1,6 @@
 """GPU tests of the measured configurations beyond the basic parity matrix.
 
-* C3: Elman at B16 N1 D768 (the cross-workgroup recurrence of a wide head), vs the oracle.
+* C3: GRU and Elman at B16 N1 D768 (the cross-workgroup recurrence of a wide head), vs the oracle.
 * C4: sLSTM B16 N4 D192 with forget bias U(3,6) and a zero start, vs the oracle
   (T=256), and at the full T=2048 through the chunk-continuation property.
 * C5: LSTM B256 N8 D128 (more groups than the GPU holds at once, so the
@@ -62,6 +62,13 @@ def strict():
 
     set_strict(True)
     yield
+
+
+def test_c3_gru_wide_head():
+    """GRU at the C3 shape: two hidden tiles per workgroup, 3 compute waves each."""
+    print("\n[C3] gru B16 T512 N1 D768", flush=True)
+    cpu, dh, dl = bf16_inputs("gru", 16, 512, 1, 768, seed=3)
+    check(gpu_run("gru", cpu, dh, dl), oracle_run("gru", cpu, dh, dl))
 
 
 def test_c3_elman_wide_head():

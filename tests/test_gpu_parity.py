@@ -71,18 +71,17 @@ CASES = [
     ("elman", 16, 16, 1, 768),
     ("slstm", 3, 7, 2, 64),
     ("slstm", 16, 32, 4, 192),
+    ("lstm", 8, 12, 1, 640),
+    ("slstm", 5, 8, 1, 576),
 ]
 
 
 @pytest.mark.parametrize("dtype", ["bfloat16", "float32"])
 @pytest.mark.parametrize("cell,B,T,N,D", CASES, ids=[f"{c[0]}-B{c[1]}T{c[2]}N{c[3]}D{c[4]}" for c in CASES])
 def test_parity_fp32_io(cell, B, T, N, D, dtype):
-    if dtype == "bfloat16" and D > 512 and cell in ("gru", "lstm", "slstm"):
-        pytest.skip("two-tile workgroups (D > 512) hold too many R^T/dG fragments for GR >= 3 in the "
-                    "current register plan; the library returns FRNN_E_UNSUPPORTED")
     if dtype == "float32" and D > 512 and cell != "elman":
         pytest.skip("FP32-operand mode holds R^T and dG fragments for D <= 512 only (register budget); "
-                    "the library returns FRNN_E_UNSUPPORTED, tested in test_gpu_api")
+                    "the library returns FRNN_E_UNSUPPORTED (see test_abi)")
     print(f"\n[parity] {cell} B{B} T{T} N{N} D{D} {dtype}", flush=True)
     actual, expected = run_pair(cell, B, T, N, D, dtype, seed=B * 1000 + D)
     names = ["states", "last", "dWx", "dR", "db", "ds0"]
