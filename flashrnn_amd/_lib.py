@@ -16,7 +16,7 @@ LIB_PATH = pathlib.Path(__file__).resolve().parent / "libfrnn.so"
 FRNN_LSTM, FRNN_GRU, FRNN_ELMAN, FRNN_SLSTM = 0, 1, 2, 3
 FRNN_F32, FRNN_BF16 = 0, 1
 FRNN_MMA_BF16, FRNN_MMA_F32 = 0, 1
-FRNN_TRAINING, FRNN_XCD_SHARED = 1, 2
+FRNN_TRAINING, FRNN_XCD_SHARED, FRNN_GRAD_CUT, FRNN_GRAD_CLIP = 1, 2, 4, 8
 FRNN_OK = 0
 FRNN_E_TIMEOUT = -5
 FRNN_E_PLACEMENT = -6
@@ -35,6 +35,7 @@ class FrnnDesc(ctypes.Structure):
         ("dtype_state", ctypes.c_int32),
         ("mma", ctypes.c_int32),
         ("flags", ctypes.c_int32),
+        ("clipval", ctypes.c_float),
     ]
 
 

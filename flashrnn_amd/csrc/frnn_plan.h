@@ -16,11 +16,14 @@ namespace frnn {
 constexpr int kXcds = 8;      // MI355X: 8 XCDs, workgroup w is dispatched to XCD w % 8
 constexpr int kMaxKT = 8;     // max 32-wide k-tiles per gate and wave (forward)
 constexpr int kMaxNFB = 32;   // max 32-wide k-tiles per wave (backward)
+// Plan flags (the C ABI's frnn_flags)
+constexpr int kFlagTraining = 1, kFlagShared = 2, kFlagCut = 4, kFlagClip = 8;
 
 struct Plan {
   int cell, B, T, N, D;
   int GR, GW, GT, S;
   int mma, dt_io, dt_state, flags;
+  float clip;      // kFlagClip: clamp bound of h and of its recurrent cotangent
   int NB;          // 16-row batch tiles per group
   int BS;          // slab rows = 16 * NB
   int nslab;       // ceil(B / BS)

@@ -655,6 +655,9 @@ __global__ void __launch_bounds__(64 * (KSC + 1) * NDT) fwd_kernel(FwdArgs a) {
         for (int g = 0; g < GR; ++g) g4[g] = xcur[g] + ry[g] + bias[s][g];
         Cell<CELL>::fwd(g4, st[s], sv, (CELL == CELL_SLSTM && t == 0) ? zflag : 0u);
       }
+      // gradient_recurrent_clipval: the new hidden state is clamped (the saved
+      // values are not: the backward passes straight through the clamp)
+      if (p.flags & kFlagClip) st[s][0] = fminf(fmaxf(st[s][0], -p.clip), p.clip);
       // the exchange word goes out first: it is what the other workgroups wait for
       if (el[s].real && t + 1 < T)
         xstore<MMA>(xc, (t & 1) * xpar + xgrp + xword_of<MMA>(p.BS, el[s].bl, el[s].d), st[s][0], step_tag(t));
@@ -805,6 +808,7 @@ __global__ void __launch_bounds__(64 * (KSC + 1) * NDT) bwd_kernel(BwdArgs a) {
   if (!team_setup(p, tm, a.status, KSC)) return;
   const int D = p.D, B = p.B, N = p.N, T = p.T;
   const int GD = GR * D;
+  const bool cut = (p.flags & kFlagCut) != 0;
 
   extern __shared__ float lds[];
   float* red = lds + tm.team * Lds<CELL, NB>::bwd(KS);  // [2][NB][64][4][KS]
@@ -904,7 +908,15 @@ __global__ void __launch_bounds__(64 * (KSC + 1) * NDT) bwd_kernel(BwdArgs a) {
       float ds[S];
 #pragma unroll
       for (int k = 0; k < S; ++k) ds[k] = carry[s][k] + in[k];
-      ds[0] += dhrec[s];
+      if (p.flags & kFlagClip) {
+        // the recurrent cotangent of h_t (direct path + R^T dG of step t+1) is
+        // clamped before the caller's cotangent is added; at the first
+        // iteration carry[0] is the caller's cotangent of the last state
+        const float rec = carry[s][0] + dhrec[s];
+        ds[0] = (it == 0 ? rec : fminf(fmaxf(rec, -p.clip), p.clip)) + in[0];
+      } else {
+        ds[0] += dhrec[s];
+      }
       float sv[NSAVE];
 #pragma unroll
       for (int v = 0; v < NSAVE; ++v) sv[v] = in[S + v];
@@ -929,7 +941,7 @@ __global__ void __launch_bounds__(64 * (KSC + 1) * NDT) bwd_kernel(BwdArgs a) {
       if constexpr (CELL == CELL_GRU) ov[3] = dry[0];
       *reinterpret_cast<f32x4*>(os + e * NOB) = ov;
       // the element's gate cotangents go out last (k = o * GR + g: one vector store when GR = 4)
-      if (el[s].real) {
+      if (el[s].real && !cut) {
         if constexpr (MMA == MMA_BF16 && GR == 4) {  // k = 4d .. 4d+3: one aligned chunk
           xstore_vec<MMA, GR>(xc, xoff + xgrp + xword_of<MMA>(p.BS, el[s].bl, el[s].d * GR), dry, step_tag(it));
         } else {
@@ -949,8 +961,10 @@ __global__ void __launch_bounds__(64 * (KSC + 1) * NDT) bwd_kernel(BwdArgs a) {
       for (int bt = 0; bt < NB; ++bt) acc[bt] = f32x4{0.f, 0.f, 0.f, 0.f};
     };
     auto prod = [&](int bt, int j, const Frag<MMA>& f) { acc[bt] = mma(A[j], f, acc[bt]); };
-    uint32_t polls;
-    if (NB == 1 && pair)
+    uint32_t polls = 0;
+    if (cut)  // gradient_recurrent_cut: no R^T dG reaches h_{t-1}
+      zero();
+    else if (NB == 1 && pair)
       polls = gather_pair_mma<MMA, NDT, NF>(xc, xword_pair, bv_pair, xoff, cstride, nkt, step_tag(it), a.status, a.spin_limit,
                                        abort, zero, prod);
     else

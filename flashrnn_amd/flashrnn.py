@@ -45,8 +45,17 @@ _IO = {torch.float32: _lib.FRNN_F32, torch.bfloat16: _lib.FRNN_BF16}
 @dataclass
 class FlashRNNConfig:
     """The subset of the reference's ``FlashRNNConfig`` (``flashrnn/flashrnn/flashrnn.py:121-380``)
-    that applies to the fused path. Options of the reference that this build
-    does not implement yet raise ``NotImplementedError`` instead of being ignored."""
+    that applies to the fused path.
+
+    ``gradient_recurrent_cut`` and ``gradient_recurrent_clipval`` behave as on
+    the reference's fused backend (``flashrnn.py:357-380, 784-787``): the cut
+    passes no ``R^T dG`` cotangent to ``h_{t-1}``; a clip value ``v`` clamps
+    every new hidden state to ``[-v, v]`` (straight-through in backward: the
+    fused build passes ``gradient_recurrent_clipval`` as its forward clip
+    value, ``flashrnn.py:368-372``) and clamps the recurrent cotangent of
+    ``h_{t-1}`` to the same interval before the caller's cotangent is added.
+    ``forward_clipval`` is accepted and, as on the reference's fused backend,
+    has no effect."""
 
     backend: str = "cuda_fused"
     function: str = "lstm"
@@ -68,8 +77,9 @@ class FlashRNNConfig:
             )
         if self.dtype not in DTYPES:
             raise ValueError(f"dtype {self.dtype!r} not supported; use one of {tuple(DTYPES)}")
-        if self.gradient_recurrent_cut or self.gradient_recurrent_clipval is not None or self.forward_clipval is not None:
-            raise NotImplementedError("gradient cut and clip options are not implemented in flashrnn_amd yet")
+        v = self.gradient_recurrent_clipval
+        if v is not None and not (float(v) >= 0.0 and float(v) < float("inf")):
+            raise ValueError(f"gradient_recurrent_clipval must be finite and >= 0, got {v}")
         (self.num_gates_r, self.num_gates_w, self.num_gates_t, self.num_states) = CELL_SIZES[self.function]
 
 
@@ -127,9 +137,12 @@ def _workspace(nbytes: int, device) -> torch.Tensor:
 
 
 # --------------------------------------------------------------------- autograd
-def _desc(cell, B, T, N, D, io, st, mma, training):
+def _desc(cell, B, T, N, D, io, st, mma, training, opts=(False, None)):
+    cut, clipval = opts
     flags = (_lib.FRNN_TRAINING if training else 0) | (_lib.FRNN_XCD_SHARED if _state["xcd_shared"] else 0)
-    return _lib.FrnnDesc(_lib.CELLS[cell], B, T, N, D, _IO[io], _IO[st], mma, flags)
+    flags |= (_lib.FRNN_GRAD_CUT if cut else 0) | (_lib.FRNN_GRAD_CLIP if clipval is not None else 0)
+    return _lib.FrnnDesc(_lib.CELLS[cell], B, T, N, D, _IO[io], _IO[st], mma, flags,
+                         float(clipval) if clipval is not None else 0.0)
 
 
 class _FusedRecurrence(torch.autograd.Function):
@@ -138,12 +151,12 @@ class _FusedRecurrence(torch.autograd.Function):
     gradients for Wx, R, b and the initial state."""
 
     @staticmethod
-    def forward(ctx, wx, R, b, s0, cell, mma):
+    def forward(ctx, wx, R, b, s0, cell, mma, opts):
         _drain_pending()
         lib = _lib.load()
         B, T, _, N, D = wx.shape
         training = torch.is_grad_enabled() or any(ctx.needs_input_grad[:4])
-        d = _desc(cell, B, T, N, D, wx.dtype, s0.dtype, mma, training)
+        d = _desc(cell, B, T, N, D, wx.dtype, s0.dtype, mma, training, opts)
         dev = wx.device
         S = CELL_SIZES[cell][3]
         states = torch.empty((S, B, T, N, D), dtype=wx.dtype, device=dev)
@@ -159,7 +172,7 @@ class _FusedRecurrence(torch.autograd.Function):
         _after_call(ws)
         if training:
             ctx.save_for_backward(R, s0, states, save)
-            ctx.meta = (cell, mma, wx.shape, wx.dtype, b.shape)
+            ctx.meta = (cell, mma, wx.shape, wx.dtype, b.shape, opts)
         return states, carry
 
     @staticmethod
@@ -167,9 +180,9 @@ class _FusedRecurrence(torch.autograd.Function):
         _drain_pending()
         lib = _lib.load()
         R, s0, states, save = ctx.saved_tensors
-        cell, mma, wshape, io, bshape = ctx.meta
+        cell, mma, wshape, io, bshape, opts = ctx.meta
         B, T, _, N, D = wshape
-        d = _desc(cell, B, T, N, D, io, s0.dtype, mma, True)
+        d = _desc(cell, B, T, N, D, io, s0.dtype, mma, True, opts)
         dev = R.device
         d_states = d_states.to(io).contiguous() if d_states is not None else None
         d_carry = d_carry.to(s0.dtype).contiguous() if d_carry is not None else None
@@ -187,7 +200,7 @@ class _FusedRecurrence(torch.autograd.Function):
         )
         _lib.check(rc, "frnn_bwd")
         _after_call(ws)
-        return dwx, dR, db, ds0, None, None
+        return dwx, dR, db, ds0, None, None, None
 
 
 # ----------------------------------------------------------------------- public API
@@ -251,7 +264,9 @@ def flashrnn(
         R = F.pad(R, (0, pad, 0, pad))
         b = F.pad(b, (0, pad))
         s0 = F.pad(s0, (0, pad))
-    hist, carry = _FusedRecurrence.apply(Wx.contiguous(), R.contiguous(), b.contiguous(), s0.contiguous(), cell, mma)
+    opts = (bool(config.gradient_recurrent_cut), config.gradient_recurrent_clipval)
+    hist, carry = _FusedRecurrence.apply(Wx.contiguous(), R.contiguous(), b.contiguous(), s0.contiguous(), cell, mma,
+                                         opts)
     if Dp != D:
         hist = hist[..., :D]
         carry = carry[..., :D]

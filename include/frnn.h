@@ -53,6 +53,17 @@ enum frnn_mma { FRNN_MMA_BF16 = 0, FRNN_MMA_F32 = 1 };
 enum frnn_flags {
   FRNN_TRAINING = 1,       /* frnn_fwd fills the saved-for-backward area */
   FRNN_XCD_SHARED = 2,     /* exchange through memory-side coherence (slower; any placement) */
+  /* The reference's FlashRNNConfig.gradient_recurrent_cut (flashrnn/flashrnn/flashrnn.py:129,
+   * 784-787; fused/flashrnn_fused_backward_cut.cu): frnn_bwd passes no R^T dG cotangent
+   * to h_{t-1}; direct paths, dR and db are unchanged. */
+  FRNN_GRAD_CUT = 4,
+  /* The reference's gradient_recurrent_clipval = clipval (flashrnn.py:131, 357-380): frnn_fwd
+   * clamps each new hidden state to [-clipval, clipval] (the fused build passes the same value
+   * as its forward clip value, flashrnn.py:368-372; the backward passes straight through the
+   * clamp), and frnn_bwd clamps the recurrent cotangent of h_{t-1} (direct path plus R^T dG)
+   * to the same interval before adding the caller's cotangent
+   * (fused/lstm_fused_pointwise.cuh:76-80, 115-124). */
+  FRNN_GRAD_CLIP = 8,
 };
 
 typedef struct frnn_desc {
@@ -65,6 +76,7 @@ typedef struct frnn_desc {
   int32_t dtype_state; /* dtype of s0, ds0, carry and d_carry */
   int32_t mma;         /* enum frnn_mma */
   int32_t flags;       /* enum frnn_flags */
+  float clipval;       /* with FRNN_GRAD_CLIP: finite and >= 0; otherwise ignored */
 } frnn_desc;
 
 enum frnn_status {

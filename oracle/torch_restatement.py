@@ -139,3 +139,103 @@ def flashrnn_torch(
         return recurrence(
             wx, recurrent, bias, initial, cell=cell, mma_dtype=mma, recurrent_mma_dtype=mma
         )
+
+
+# ----------------------------------------------------------------------------
+# Options of the reference's fused (v1) backend, restated on top of the
+# flashrnn_torch cell above. flashrnn_torch itself has none of them; their
+# semantics come from the v1 CUDA pointwise code and its build flags:
+#
+# * gradient_recurrent_clipval = v (``flashrnn/flashrnn/flashrnn.py:357-380``).
+#   The build passes v as BOTH -DFLASHRNN_GRADIENT_RECURRENT_CLIPVAL and
+#   -DFLASHRNN_FORWARD_CLIPVAL (``flashrnn.py:368-372`` reads
+#   gradient_recurrent_clipval for the forward value too), so:
+#     - forward: the new hidden state is clamped to [-v, v] after the cell
+#       and the clamped value is both output and recurrent input
+#       (``fused/lstm_fused_pointwise.cuh:76-80``; gru :76-80, elman :51-55,
+#       slstm :100-104); the backward has no clamp mask (straight through);
+#     - backward: the recurrent cotangent of h_{t-1} -- everything that
+#       reaches h_{t-1} through step t (R^T dG plus the cell's direct path,
+#       e.g. GRU's u * dh) -- is clamped to [-v, v] before the cotangent from
+#       the caller is added (``lstm_fused_pointwise.cuh:115-124``); the
+#       cotangent of the initial state is returned unclamped.
+# * forward_clipval: not read by the fused build (see above), so no effect.
+# * gradient_recurrent_cut (``flashrnn.py:784-787``,
+#   ``fused/flashrnn_fused_backward_cut.cu:92-181``): the backward loop is
+#   pointwise only -- no R^T dG reaches h_{t-1}; direct paths (c, n, GRU's
+#   u * dh) and dR, db are unchanged.
+#
+# Parity of this restatement is pinned by tests/test_oracle.py (closed forms
+# and cross-checks between the options), as no golden vectors exist for them.
+class _ClampGrad(torch.autograd.Function):
+    """Identity forward; backward clamps the cotangent to [-v, v]."""
+
+    @staticmethod
+    def forward(ctx, x, v):
+        ctx.v = v
+        return x.view_as(x)
+
+    @staticmethod
+    def backward(ctx, g):
+        return g.clamp(-ctx.v, ctx.v), None
+
+
+class _StraightClamp(torch.autograd.Function):
+    """Forward clamps to [-v, v]; backward passes the cotangent unchanged."""
+
+    @staticmethod
+    def forward(ctx, x, v):
+        return x.clamp(-v, v)
+
+    @staticmethod
+    def backward(ctx, g):
+        return g, None
+
+
+def recurrence_fused_options(
+    wx: torch.Tensor,
+    recurrent: torch.Tensor,
+    bias: torch.Tensor,
+    initial: torch.Tensor,
+    cell: str = "lstm",
+    mma_dtype: torch.dtype | None = None,
+    gradient_recurrent_cut: bool = False,
+    gradient_recurrent_clipval: float | None = None,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """``recurrence`` with the fused backend's cut / clip options (see above)."""
+    state = initial[:, :, 0]
+    history = []
+    v = gradient_recurrent_clipval
+    for step, x in enumerate(wx.unbind(1)):
+        carried = state
+        if v is not None and step > 0:
+            # the recurrent cotangent of h_{t-1}: both uses inside this step. The
+            # initial state's cotangent is returned unclamped (the clamp runs at
+            # the start of the next pointwise step, and step 0 has none:
+            # fused/flashrnn_fused_backward.cu:612-621 stores ds_inout as is)
+            carried = torch.cat((_ClampGrad.apply(state[:1], float(v)), state[1:]))
+        h_in = carried[0].detach() if gradient_recurrent_cut else carried[0]
+        hidden = _round_through(h_in, mma_dtype)
+        weight = _round_through(recurrent, mma_dtype)
+        ry = torch.einsum("bnp,gnop->bgno", hidden, weight)
+        state = _cell_step(cell, x, ry, bias, carried)
+        if v is not None:  # forward clamp, straight-through backward
+            state = torch.cat((_StraightClamp.apply(state[:1], float(v)), state[1:]))
+        history.append(state)
+    return torch.stack(history, dim=2), state.unsqueeze(2)
+
+
+def flashrnn_torch_fused_options(
+    wx, recurrent, bias, initial, *, cell="lstm", numerics="mathematical",
+    gradient_recurrent_cut=False, gradient_recurrent_clipval=None,
+):
+    """``flashrnn_torch`` semantics plus the fused backend's cut / clip options."""
+    if cell not in SIZES:
+        raise ValueError(f"unsupported cell: {cell}")
+    mma = torch.bfloat16 if numerics == "fp32_state_bf16_mma" else None
+    with torch.autocast(wx.device.type, enabled=False):
+        return recurrence_fused_options(
+            wx, recurrent, bias, initial, cell=cell, mma_dtype=mma,
+            gradient_recurrent_cut=gradient_recurrent_cut,
+            gradient_recurrent_clipval=gradient_recurrent_clipval,
+        )

@@ -32,8 +32,8 @@ def lib():
 
 
 def desc(cell="lstm", B=8, T=1024, N=3, D=256, io=_lib.FRNN_BF16, st=_lib.FRNN_F32, mma=_lib.FRNN_MMA_BF16,
-         flags=_lib.FRNN_TRAINING):
-    return _lib.FrnnDesc(_lib.CELLS[cell], B, T, N, D, io, st, mma, flags)
+         flags=_lib.FRNN_TRAINING, clipval=0.0):
+    return _lib.FrnnDesc(_lib.CELLS[cell], B, T, N, D, io, st, mma, flags, clipval)
 
 
 def test_header_declares_the_bound_exports():
@@ -104,6 +104,23 @@ def test_width_support(lib, cell, D, mma, ok):
     assert (lib.frnn_workspace_bytes(ctypes.byref(d), 0) > 0) == ok
 
 
+@pytest.mark.parametrize(
+    "flags,clipval,ok",
+    [
+        (_lib.FRNN_GRAD_CUT, 0.0, True), (_lib.FRNN_GRAD_CLIP, 0.25, True), (_lib.FRNN_GRAD_CLIP, 0.0, True),
+        (_lib.FRNN_GRAD_CUT | _lib.FRNN_GRAD_CLIP, 1.0, True), (_lib.FRNN_GRAD_CLIP, -0.5, False),
+        (_lib.FRNN_GRAD_CLIP, float("nan"), False), (_lib.FRNN_GRAD_CLIP, float("inf"), False),
+        (64, 0.0, False), (0, -3.0, True),  # without FRNN_GRAD_CLIP the value is ignored
+    ],
+)
+def test_option_flags(lib, flags, clipval, ok):
+    """gradient_recurrent_cut / gradient_recurrent_clipval in the descriptor."""
+    d = desc(flags=_lib.FRNN_TRAINING | flags, clipval=clipval)
+    assert (lib.frnn_workspace_bytes(ctypes.byref(d), 0) > 0) == ok
+    if not ok:
+        assert lib.frnn_fwd(ctypes.byref(d), *([None] * 8), 0, None) == -1
+
+
 def test_null_pointers_rejected_before_launch(lib):
     d = desc(B=2, T=4, N=1, D=64)
     assert lib.frnn_fwd(ctypes.byref(d), *([None] * 8), 0, None) == -1
@@ -132,8 +149,10 @@ def test_config_validation():
         FlashRNNConfig(backend="vanilla")
     with pytest.raises(ValueError):
         FlashRNNConfig(dtype="float16")
-    with pytest.raises(NotImplementedError):
-        FlashRNNConfig(gradient_recurrent_clipval=1.0)
+    for bad in (-1.0, float("nan"), float("inf")):
+        with pytest.raises(ValueError, match="clipval"):
+            FlashRNNConfig(gradient_recurrent_clipval=bad)
+    FlashRNNConfig(gradient_recurrent_clipval=0.5, gradient_recurrent_cut=True, forward_clipval=3.0)
     c = FlashRNNConfig(function="slstm")
     assert (c.num_gates_r, c.num_gates_w, c.num_gates_t, c.num_states) == (4, 4, 4, 4)
 
