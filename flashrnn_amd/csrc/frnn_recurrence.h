@@ -40,13 +40,18 @@ struct BwdRing {  // input steps staged ahead, bounded by the I/O wave's registe
 };
 
 // LDS layout of a team:
-//   forward : red  [2][KS][NB][64 lanes][4 regs][4 gates]  MFMA partial sums
+//   forward : red  [2][KS][NB][272 slots][4 gates]        MFMA partial sums; slot
+//                  red_slot(lane*4 + reg): one spare slot per 16, so both the
+//                  16-byte writes (lane-major) and the owners' reads (element-
+//                  major) hit 16 distinct bank groups per 16 lanes
 //             xring[slot][gate][64 chunks][16 bytes]       raw Wx of the next steps
 //                  (chunk = row * 4 + quad: FP32 units 4*quad..+3; BF16 units
 //                   4*quad..+7 in the even quads, odd quads unused)
 //             ost  [2][value][NE]                         states + saved values,
 //                  value-major so the drain reads 4 elements per 16-byte read
-//   backward: red  [2][NB][64 lanes][4 regs][KS]          partial R^T dG
+//   backward: red  [2][NB][KS][304]                       partial R^T dG at
+//                  red_idx(lane*4 + reg): 16 spare floats per 64, so the
+//                  16-byte writes and the owners' scalar reads are conflict-free
 //             iring[P][NE][NOP]                           state cotangents + saved values
 //             ost  [2][NE][4]                             dWx (+ GRU candidate cotangent)
 template <int CELL, int NB>
@@ -59,13 +64,19 @@ struct Lds {
   // floats per team
   static constexpr int NV = S + NSAVE;                      // staged values per element (forward)
   static constexpr int RING = GW * 64 * 4;                   // floats per Wx ring slot
+  static constexpr int RED_F = 272 * 4;  // floats per (wave, batch tile), forward partials
+  static constexpr int RED_B = 304;      // floats per (batch tile, wave), backward partials
   __host__ __device__ static constexpr long fwd(int KS) {
-    return 2L * KS * NB * 1024 + (long)kFwdRing * RING + 2L * NV * NE;
+    return 2L * KS * NB * RED_F + (long)kFwdRing * RING + 2L * NV * NE;
   }
   __host__ __device__ static constexpr long bwd(int KS) {
-    return 2L * NB * 256 * KS + (long)BwdRing<CELL>::P * NE * NOP + 2L * NE * NOB;
+    return 2L * NB * KS * RED_B + (long)BwdRing<CELL>::P * NE * NOP + 2L * NE * NOB;
   }
 };
+
+// Padded positions of the partial-sum layouts (see Lds).
+__device__ __forceinline__ int red_slot(int s) { return s + (s >> 4); }
+__device__ __forceinline__ int red_idx(int s) { return s + (s >> 6) * 16; }
 
 struct Team {
   int lane, w, row, kq;  // lane in wave, wave in workgroup, lane%16, lane/16
@@ -480,8 +491,9 @@ __global__ void __launch_bounds__(64 * (KSC + 1) * NDT) fwd_kernel(FwdArgs a) {
   const int D = p.D, B = p.B, T = p.T, N = p.N;
 
   extern __shared__ float lds[];
-  float* red = lds + tm.team * Lds<CELL, NB>::fwd(KS);  // [2][KS][NB][64][4][4]
-  float* xring = red + 2L * KS * NB * 1024;             // [slot][gate][64][4]
+  constexpr int RED_F = Lds<CELL, NB>::RED_F;
+  float* red = lds + tm.team * Lds<CELL, NB>::fwd(KS);  // [2][KS][NB][272][4]
+  float* xring = red + 2L * KS * NB * RED_F;            // [slot][gate][64][4]
   float* ost = xring + (long)kFwdRing * RING;           // [2][NV][NE]
 
   // sLSTM: the reference's global predicate all(n0 == 0) over the call's whole initial state
@@ -610,7 +622,7 @@ __global__ void __launch_bounds__(64 * (KSC + 1) * NDT) fwd_kernel(FwdArgs a) {
     }
     prof.mark(0);
     prof.stamp(t, 1);
-    float* rp = red + (long)(t & 1) * KS * NB * 1024;
+    float* rp = red + (long)(t & 1) * KS * NB * RED_F;
 #pragma unroll
     for (int bt = 0; bt < NB; ++bt)
 #pragma unroll
@@ -618,7 +630,7 @@ __global__ void __launch_bounds__(64 * (KSC + 1) * NDT) fwd_kernel(FwdArgs a) {
         f32x4 v = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int g = 0; g < GR; ++g) v[g] = acc[bt][g][i];
-        *reinterpret_cast<f32x4*>(rp + (((tm.kw * NB + bt) * 64 + tm.lane) * 4 + i) * 4) = v;
+        *reinterpret_cast<f32x4*>(rp + (tm.kw * NB + bt) * RED_F + red_slot(tm.lane * 4 + i) * 4) = v;
       }
     prof.mark(1);
     __syncthreads();
@@ -631,10 +643,10 @@ __global__ void __launch_bounds__(64 * (KSC + 1) * NDT) fwd_kernel(FwdArgs a) {
     for (int s = 0; s < EPLMAX; ++s) {
       if (!own[s]) continue;
       const int e = oe[s];
-      const int src = ((e >> 8) * 64 * 4 + mfma_pos(e)) * 4;  // [bt][lane][reg] -> 4 gates
+      const int src = (e >> 8) * RED_F + red_slot(mfma_pos(e)) * 4;  // [bt][slot] -> 4 gates
       f32x4 part[KS];
 #pragma unroll
-      for (int w2 = 0; w2 < KS; ++w2) part[w2] = *reinterpret_cast<const f32x4*>(rp + w2 * NB * 1024 + src);
+      for (int w2 = 0; w2 < KS; ++w2) part[w2] = *reinterpret_cast<const f32x4*>(rp + w2 * NB * RED_F + src);
       float xcur[GW];
 #pragma unroll
       for (int g = 0; g < GW; ++g) xcur[g] = xnext[s][g];
@@ -811,8 +823,9 @@ __global__ void __launch_bounds__(64 * (KSC + 1) * NDT) bwd_kernel(BwdArgs a) {
   const bool cut = (p.flags & kFlagCut) != 0;
 
   extern __shared__ float lds[];
-  float* red = lds + tm.team * Lds<CELL, NB>::bwd(KS);  // [2][NB][64][4][KS]
-  float* iring = red + 2L * NB * 256 * KS;               // [P][NE][NOP]
+  constexpr int RED_B = Lds<CELL, NB>::RED_B;
+  float* red = lds + tm.team * Lds<CELL, NB>::bwd(KS);  // [2][NB][KS][304]
+  float* iring = red + 2L * NB * KS * RED_B;             // [P][NE][NOP]
   float* ost = iring + (long)P * NE * NOP;               // [2][NE][NOB]
 
   if (tm.kw == KS) {
@@ -973,11 +986,10 @@ __global__ void __launch_bounds__(64 * (KSC + 1) * NDT) bwd_kernel(BwdArgs a) {
     prof.add(4, polls);
     prof.mark(0);
     prof.stamp(it, 2);
-    float* rp = red + (long)(it & 1) * NB * 256 * KS;
+    float* rp = red + (long)(it & 1) * NB * KS * RED_B;
 #pragma unroll
     for (int bt = 0; bt < NB; ++bt)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) rp[((bt * 64 + tm.lane) * 4 + i) * KS + tm.kw] = acc[bt][i];
+      *reinterpret_cast<f32x4*>(rp + (bt * KS + tm.kw) * RED_B + red_idx(tm.lane * 4)) = acc[bt];
     prof.mark(1);
     __syncthreads();
     prof.mark(2);
@@ -987,19 +999,10 @@ __global__ void __launch_bounds__(64 * (KSC + 1) * NDT) bwd_kernel(BwdArgs a) {
 #pragma unroll
     for (int s = 0; s < EPLMAX; ++s) {
       if (!own[s]) continue;
-      const int src = ((oe[s] >> 8) * 256 + mfma_pos(oe[s])) * KS;
+      const int src = (oe[s] >> 8) * KS * RED_B + red_idx(mfma_pos(oe[s]));
       float part[KS];
-      if constexpr (KS % 4 == 0) {
 #pragma unroll
-        for (int c = 0; c < KS / 4; ++c) {
-          const f32x4 v4 = *reinterpret_cast<const f32x4*>(rp + src + 4 * c);
-#pragma unroll
-          for (int r = 0; r < 4; ++r) part[4 * c + r] = v4[r];
-        }
-      } else {
-#pragma unroll
-        for (int w2 = 0; w2 < KS; ++w2) part[w2] = rp[src + w2];
-      }
+      for (int w2 = 0; w2 < KS; ++w2) part[w2] = rp[src + w2 * RED_B];
       float v = 0.f;
 #pragma unroll
       for (int w2 = 0; w2 < KS; ++w2) v += part[w2];

@@ -3,12 +3,15 @@
 Usage (after the rocprofv3 runs listed in each summary's header)::
 
     python -m flashrnn_amd.rocprof_summary --workload NAME --cmd "..." \
-        --kernel-trace DIR [--fetch DIR --write DIR --copy-fetch DIR --copy-write DIR --copy-mib M] --out profiles/
+        --kernel-trace DIR [--fetch DIR --write DIR --copy-fetch DIR --copy-write DIR --copy-mib M]
+        [--sq DIR --active-cus C] --out profiles/
 
 The kernel-trace summary lists per-kernel call counts and durations. The
 traffic summary gives each kernel's FETCH_SIZE / WRITE_SIZE per dispatch
 (KiB, as the counters read) and the bytes they stand for, after scaling each
-counter by what it reads for a plain device copy of known size.
+counter by what it reads for a plain device copy of known size. The SQ
+summary gives MFMA busy cycles and FLOP, the MFMA busy fraction of the CUs the
+recurrence occupies, and LDS bank conflicts.
 """
 
 from __future__ import annotations
@@ -56,6 +59,11 @@ def main(argv=None):
     ap.add_argument("--copy-fetch")
     ap.add_argument("--copy-write")
     ap.add_argument("--copy-mib", type=int, default=512)
+    ap.add_argument("--sq", help="counter CSVs of one pass over SQ_VALU_MFMA_BUSY_CYCLES, "
+                    "SQ_INSTS_VALU_MFMA_MOPS_BF16, SQ_LDS_BANK_CONFLICT, SQ_LDS_IDX_ACTIVE, SQ_INSTS_LDS, "
+                    "SQ_BUSY_CU_CYCLES, GRBM_GUI_ACTIVE")
+    ap.add_argument("--active-cus", type=int, default=48, help="CUs the persistent kernels occupy")
+    ap.add_argument("--clock-mhz", type=float, default=2400.0)
     ap.add_argument("--out", default="profiles")
     a = ap.parse_args(argv)
 
@@ -90,6 +98,34 @@ def main(argv=None):
         p2 = os.path.join(a.out, f"hbm_traffic_{a.workload}.txt")
         open(p2, "w").write("\n".join(lines) + "\n")
         print(p2)
+
+    if a.sq:
+        names = ["SQ_VALU_MFMA_BUSY_CYCLES", "SQ_INSTS_VALU_MFMA_MOPS_BF16", "SQ_LDS_BANK_CONFLICT",
+                 "SQ_LDS_IDX_ACTIVE", "SQ_INSTS_LDS", "SQ_BUSY_CU_CYCLES", "GRBM_GUI_ACTIVE"]
+        c = {n: counter(a.sq, n) for n in names}
+        dur = {n: avg for n, _, avg, *_ in stats}
+        lines = [f"# SQ counters per dispatch: {a.workload}", "", "Command:", "",
+                 *[f"    {x}" for x in a.cmd.split(";;")], "",
+                 "Columns: MFMA busy cycles (summed over SIMDs) and BF16 MFMA FLOP (MOPS x 512); MFMA busy",
+                 f"fraction of the SIMDs of the {a.active_cus} CUs the recurrence occupies over the kernel's traced",
+                 f"duration at {a.clock_mhz:.0f} MHz (whole chip: x {a.active_cus}/256); LDS bank-conflict cycles,",
+                 "and conflict cycles per conflict-free LDS cycle (SQ_LDS_BANK_CONFLICT / (SQ_LDS_IDX_ACTIVE -",
+                 "SQ_LDS_BANK_CONFLICT)); LDS instructions.", "",
+                 f"{'kernel':40s} {'mfma_busy':>12s} {'bf16_GFLOP':>11s} {'busy_frac':>9s} {'lds_conflict':>13s} "
+                 f"{'confl_ratio':>11s} {'lds_insts':>11s}"]
+        for n in c["SQ_VALU_MFMA_BUSY_CYCLES"]:
+            busy = c["SQ_VALU_MFMA_BUSY_CYCLES"][n]
+            flop = c["SQ_INSTS_VALU_MFMA_MOPS_BF16"].get(n, 0.0) * 512
+            conf = c["SQ_LDS_BANK_CONFLICT"].get(n, 0.0)
+            act = c["SQ_LDS_IDX_ACTIVE"].get(n, 0.0)
+            ratio = conf / (act - conf) if act > conf else 0.0
+            d = dur.get(n)
+            frac = busy / (d * 1e-3 * a.clock_mhz * 4 * a.active_cus) if d else float("nan")
+            lines.append(f"{n[:40]:40s} {busy:12.0f} {flop / 1e9:11.3f} {frac:9.4f} {conf:13.0f} {ratio:11.4f} "
+                         f"{c['SQ_INSTS_LDS'].get(n, 0.0):11.0f}")
+        p3 = os.path.join(a.out, f"sq_counters_{a.workload}.txt")
+        open(p3, "w").write("\n".join(lines) + "\n")
+        print(p3)
 
 
 if __name__ == "__main__":
