@@ -214,7 +214,7 @@ def main(argv=None):
         result["phases_cycles_per_step"] = out
         if args.trace_out:
             import numpy as np
-            np.save(args.trace_out, np.array(v[256:], dtype=np.int64).reshape(2, 128, 16, 16, 4))
+            np.save(args.trace_out, np.array(v[256:], dtype=np.int64).reshape(2, 128, 16, 8, 8))
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(torch)
     print(json.dumps(result), flush=True)

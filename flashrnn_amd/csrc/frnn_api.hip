@@ -139,7 +139,8 @@ int make_plan(const frnn_desc* d, Plan* p) {
   p->dt_io = d->dtype_io;
   p->dt_state = d->dtype_state;
   p->flags = d->flags;
-  if (d->flags & ~(FRNN_TRAINING | FRNN_XCD_SHARED | FRNN_GRAD_CUT | FRNN_GRAD_CLIP)) return FRNN_E_INVALID;
+  if (d->flags & ~(FRNN_TRAINING | FRNN_XCD_SHARED | FRNN_GRAD_CUT | FRNN_GRAD_CLIP | FRNN_TEST_UNREADY))
+    return FRNN_E_INVALID;
   if (d->flags & FRNN_GRAD_CLIP) {
     if (!(d->clipval >= 0.f) || d->clipval > 3.4e38f) return FRNN_E_INVALID;  // NaN, negative or infinite
     p->clip = d->clipval;

@@ -300,6 +300,17 @@ __device__ __forceinline__ void raise_status(uint32_t* status, uint32_t code) {
   atomicMax(status, code);
 }
 
+// Workgroup barrier that orders LDS only. __syncthreads() also waits for
+// every outstanding global load and store of the wave (vmcnt(0)), which would
+// make the I/O waves wait for the HBM loads they issue steps ahead; the
+// recurrence kernels exchange data between waves through LDS only, and wait
+// for their own global loads explicitly where they need them.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 __device__ __forceinline__ uint32_t xcc_id() {
   uint32_t v;
   asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(v));

@@ -17,7 +17,7 @@ constexpr int kXcds = 8;      // MI355X: 8 XCDs, workgroup w is dispatched to XC
 constexpr int kMaxKT = 8;     // max 32-wide k-tiles per gate and wave (forward)
 constexpr int kMaxNFB = 32;   // max 32-wide k-tiles per wave (backward)
 // Plan flags (the C ABI's frnn_flags)
-constexpr int kFlagTraining = 1, kFlagShared = 2, kFlagCut = 4, kFlagClip = 8;
+constexpr int kFlagTraining = 1, kFlagShared = 2, kFlagCut = 4, kFlagClip = 8, kFlagUnready = 16;
 
 struct Plan {
   int cell, B, T, N, D;

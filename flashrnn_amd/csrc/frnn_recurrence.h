@@ -74,6 +74,12 @@ struct Lds {
   }
 };
 
+// Tag a poll waits for: the step's, or (kFlagUnready, failure-handling tests)
+// 3, which is never written.
+__device__ __forceinline__ uint32_t ptag(const Plan& p, int step) {
+  return (p.flags & kFlagUnready) ? 3u : step_tag(step);
+}
+
 // Padded positions of the partial-sum layouts (see Lds).
 __device__ __forceinline__ int red_slot(int s) { return s + (s >> 4); }
 __device__ __forceinline__ int red_idx(int s) { return s + (s >> 6) * 16; }
@@ -137,7 +143,7 @@ __device__ __forceinline__ long save_index(const Plan& p, int ne, int t, int wgi
 // (waits for its loads), [1] load issue, [2] barrier, [3] output drain, [5] steps.
 //
 // With profiling on, every wave of every workgroup also keeps a timeline of
-// steps kTraceT0 .. kTraceT0+15: four stamps per step from the chip-wide
+// steps kTraceT0 .. kTraceT0+7: eight stamps per step from the chip-wide
 // 100 MHz clock (s_memrealtime), lane `slot` holding stamp `slot`, written
 // after the loop to trace[(workgroup * 16 + wave) * 64 + lane].
 constexpr int kTraceT0 = 64;
@@ -155,7 +161,7 @@ struct Prof {
   }
   __device__ __forceinline__ void stamp(int step, int k) {
     if (!tr) return;
-    const int slot = (step - kTraceT0) * 4 + k;
+    const int slot = (step - kTraceT0) * 8 + k;
     if (slot < 0 || slot >= 64) return;
     const unsigned long long now = __builtin_amdgcn_s_memrealtime();
     if ((int)(threadIdx.x & 63) == slot) tv = now;
@@ -397,9 +403,9 @@ __device__ __forceinline__ float ring_x(const float* slot, int g, int r, int d, 
 // u % kFwdRing by LDS-DMA (global_load_lds: no registers in flight), issued
 // kFwdAhead steps ahead; before barrier t the wave waits, by count, until the
 // loads of step t+1 have landed, so the owners read step t+1's Wx right after
-// their step-t cell, off the critical path. After barrier t it drains the
-// outputs of step t-1, then issues the loads of step t+kFwdAhead. Per step the
-// wave issues the same stores and loads in the same order, so the count of
+// their step-t cell, off the critical path. It then issues the loads of step
+// t+kFwdAhead and, after barrier t, drains the outputs of step t-1. Per step
+// the wave issues the same loads and stores in the same order, so the count of
 // operations issued after a step's loads is a constant in the steady state
 // (the first and last steps wait for everything). Padding batch rows are
 // neither loaded nor stored.
@@ -443,8 +449,10 @@ __device__ void fwd_io(const FwdArgs& a, const Team& tm, float* xring, float* os
         *reinterpret_cast<f32x4*>(a.save + save_index(p, NE, t, tm.wgi, v - S, tm.team, e0)) = x;
     }
   };
-  // VMEM operations issued after the loads of step t+1, at the top of
-  // iteration t (steady state): P-2 iterations of stores and loads
+  // Per iteration t: wait for the loads of step t+1; barrier t; drain step
+  // t-1; issue the loads of step t+P. VMEM operations issued after the loads
+  // of step t+1, at the top of iteration t (steady state): P-2 iterations of
+  // stores and loads.
   static_assert(P >= 2, "prefetch distance");
   constexpr int kAfterTrain = (P - 2) * (GW + NV), kAfterInfer = (P - 2) * (GW + S);
 
@@ -452,7 +460,7 @@ __device__ void fwd_io(const FwdArgs& a, const Team& tm, float* xring, float* os
   prof.init(a.prof != nullptr && blockIdx.x == 0, a.prof != nullptr);
   for (int u = 0; u < P && u < T; ++u) load_wx(u);
   wait_vm<0>();
-  __syncthreads();  // Wx_0 in its slot
+  lds_barrier();  // Wx_0 in its slot
   for (int t = 0; t < T; ++t) {
     if (t + 1 >= P && t + P <= T) {
       if (training) wait_vm<kAfterTrain>();
@@ -464,15 +472,17 @@ __device__ void fwd_io(const FwdArgs& a, const Team& tm, float* xring, float* os
     prof.stamp(t, 0);
     prof.mark(1);
     prof.stamp(t, 1);
-    __syncthreads();  // step t: Wx_{t+1} in its slot; outputs of step t-1 staged
+    lds_barrier();  // step t: Wx_{t+1} in its slot; outputs of step t-1 staged
     prof.mark(2);
     prof.stamp(t, 2);
     if (t >= 1) store_out(t - 1, ost + ((t - 1) & 1) * NV * NE);
+    // slot (t+P) % kFwdRing held step t-1, which every owner finished reading
+    // before barrier t-1
     if (t + P < T) load_wx(t + P);
     prof.mark(3);
     prof.stamp(t, 3);
   }
-  __syncthreads();  // outputs of the last step complete
+  lds_barrier();  // outputs of the last step complete
   store_out(T - 1, ost + ((T - 1) & 1) * NV * NE);
   prof.acc[5] = T;
   prof.flush(a.prof);
@@ -583,7 +593,7 @@ __global__ void __launch_bounds__(64 * (KSC + 1) * NDT) fwd_kernel(FwdArgs a) {
   // load still pending at the loop head, and does not fence the exchange
   // stores inside the loop behind one.
   __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();  // Wx_0 in its slot
+  lds_barrier();  // Wx_0 in its slot
   // Wx of the next step, read from the ring right after each cell
   float xnext[EPLMAX][GW];
   auto read_x = [&](int u) {
@@ -613,11 +623,11 @@ __global__ void __launch_bounds__(64 * (KSC + 1) * NDT) fwd_kernel(FwdArgs a) {
       uint32_t polls;
       const int off = ((t - 1) & 1) * xpar;
       if (NB == 1 && pair)
-        polls = gather_pair_mma<MMA, NDT, KTW>(xc, xword_pair, bv_pair, off, cstride, nkt, step_tag(t - 1), a.status, a.spin_limit,
-                                          abort, zero, prod);
+        polls = gather_pair_mma<MMA, NDT, KTW>(xc, xword_pair, bv_pair, off, cstride, nkt, ptag(p, t - 1), a.status,
+                                               a.spin_limit, abort, zero, prod);
       else
-        polls = gather_mma<MMA, NDT, NB, KTW>(xc, xword, bval, off, cstride, nkt, step_tag(t - 1), a.status, a.spin_limit, abort,
-                                         zero, prod);
+        polls = gather_mma<MMA, NDT, NB, KTW>(xc, xword, bval, off, cstride, nkt, ptag(p, t - 1), a.status,
+                                              a.spin_limit, abort, zero, prod);
       prof.add(4, polls);
     }
     prof.mark(0);
@@ -633,7 +643,7 @@ __global__ void __launch_bounds__(64 * (KSC + 1) * NDT) fwd_kernel(FwdArgs a) {
         *reinterpret_cast<f32x4*>(rp + (tm.kw * NB + bt) * RED_F + red_slot(tm.lane * 4 + i) * 4) = v;
       }
     prof.mark(1);
-    __syncthreads();
+    lds_barrier();
     prof.mark(2);
     prof.stamp(t, 2);
 
@@ -673,6 +683,7 @@ __global__ void __launch_bounds__(64 * (KSC + 1) * NDT) fwd_kernel(FwdArgs a) {
       // the exchange word goes out first: it is what the other workgroups wait for
       if (el[s].real && t + 1 < T)
         xstore<MMA>(xc, (t & 1) * xpar + xgrp + xword_of<MMA>(p.BS, el[s].bl, el[s].d), st[s][0], step_tag(t));
+      if (s == 0) prof.stamp(t, 3);
 #pragma unroll
       for (int k = 0; k < S; ++k) os[k * NE + e] = st[s][k];
 #pragma unroll
@@ -680,9 +691,9 @@ __global__ void __launch_bounds__(64 * (KSC + 1) * NDT) fwd_kernel(FwdArgs a) {
     }
     if (t + 1 < T) read_x(t + 1);  // landed before barrier t
     prof.mark(3);
-    prof.stamp(t, 3);
+    prof.stamp(t, 4);
   }
-  __syncthreads();  // the I/O wave drains the last step
+  lds_barrier();  // the I/O wave drains the last step
 
   // ---- carry: the last state in full precision
   if (a.carry) {
@@ -778,7 +789,7 @@ __device__ void bwd_io(const BwdArgs& a, const Team& tm, float* iring, float* os
     if (j < T) load_in(j, buf[j]);
   stage(0, buf[0]);
   if (P < T) load_in(P, buf[0]);
-  __syncthreads();  // iteration 0's inputs staged
+  lds_barrier();  // iteration 0's inputs staged
   for (int it0 = 0; it0 < T; it0 += P) {
 #pragma unroll
     for (int j = 0; j < P; ++j) {
@@ -793,7 +804,7 @@ __device__ void bwd_io(const BwdArgs& a, const Team& tm, float* iring, float* os
           prof.mark(1);
           prof.stamp(it, 1);
         }
-        __syncthreads();  // iteration it: outputs staged; inputs of it+1 staged
+        lds_barrier();  // iteration it: outputs staged; inputs of it+1 staged
         prof.mark(2);
         prof.stamp(it, 2);
         store_out(it, ost + (long)(it & 1) * NOB * NE);
@@ -899,7 +910,7 @@ __global__ void __launch_bounds__(64 * (KSC + 1) * NDT) bwd_kernel(BwdArgs a) {
   Prof prof;
   prof.init(a.prof != nullptr && blockIdx.x == 0, a.prof != nullptr);
   __builtin_amdgcn_s_waitcnt(0);  // no set-up load pending at the loop head (see the forward kernel)
-  __syncthreads();  // iteration 0's inputs staged by the I/O wave
+  lds_barrier();  // iteration 0's inputs staged by the I/O wave
   bool abort = false;
   for (int it = 0; it < T; ++it) {
     prof.stamp(it, 0);
@@ -978,11 +989,11 @@ __global__ void __launch_bounds__(64 * (KSC + 1) * NDT) bwd_kernel(BwdArgs a) {
     if (cut)  // gradient_recurrent_cut: no R^T dG reaches h_{t-1}
       zero();
     else if (NB == 1 && pair)
-      polls = gather_pair_mma<MMA, NDT, NF>(xc, xword_pair, bv_pair, xoff, cstride, nkt, step_tag(it), a.status, a.spin_limit,
-                                       abort, zero, prod);
+      polls = gather_pair_mma<MMA, NDT, NF>(xc, xword_pair, bv_pair, xoff, cstride, nkt, ptag(p, it), a.status,
+                                            a.spin_limit, abort, zero, prod);
     else
-      polls = gather_mma<MMA, NDT, NB, NF>(xc, xword, bval, xoff, cstride, nkt, step_tag(it), a.status, a.spin_limit, abort, zero,
-                                      prod);
+      polls = gather_mma<MMA, NDT, NB, NF>(xc, xword, bval, xoff, cstride, nkt, ptag(p, it), a.status, a.spin_limit,
+                                           abort, zero, prod);
     prof.add(4, polls);
     prof.mark(0);
     prof.stamp(it, 2);
@@ -991,7 +1002,7 @@ __global__ void __launch_bounds__(64 * (KSC + 1) * NDT) bwd_kernel(BwdArgs a) {
     for (int bt = 0; bt < NB; ++bt)
       *reinterpret_cast<f32x4*>(rp + (bt * KS + tm.kw) * RED_B + red_idx(tm.lane * 4)) = acc[bt];
     prof.mark(1);
-    __syncthreads();
+    lds_barrier();
     prof.mark(2);
     prof.stamp(it, 3);
 
@@ -1010,6 +1021,7 @@ __global__ void __launch_bounds__(64 * (KSC + 1) * NDT) bwd_kernel(BwdArgs a) {
       dhrec[s] = el[s].real ? (MMA == MMA_BF16 ? round_bf16(v) : v) : 0.f;
     }
     prof.mark(6);
+    prof.stamp(it, 4);
   }
 
   // ---- d(initial state), d(bias) partials

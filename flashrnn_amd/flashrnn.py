@@ -85,7 +85,8 @@ class FlashRNNConfig:
 
 # ----------------------------------------------------------------- status handling
 _state = {"xcd_shared": os.environ.get("FRNN_XCD_SHARED", "0") == "1",
-          "strict": os.environ.get("FRNN_SYNC_CHECK", "0") == "1"}
+          "strict": os.environ.get("FRNN_SYNC_CHECK", "0") == "1",
+          "test_unready": False}  # failure-handling tests only (FRNN_TEST_UNREADY)
 _pending: collections.deque = collections.deque()
 
 
@@ -141,6 +142,7 @@ def _desc(cell, B, T, N, D, io, st, mma, training, opts=(False, None)):
     cut, clipval = opts
     flags = (_lib.FRNN_TRAINING if training else 0) | (_lib.FRNN_XCD_SHARED if _state["xcd_shared"] else 0)
     flags |= (_lib.FRNN_GRAD_CUT if cut else 0) | (_lib.FRNN_GRAD_CLIP if clipval is not None else 0)
+    flags |= _lib.FRNN_TEST_UNREADY if _state["test_unready"] else 0
     return _lib.FrnnDesc(_lib.CELLS[cell], B, T, N, D, _IO[io], _IO[st], mma, flags,
                          float(clipval) if clipval is not None else 0.0)
 

@@ -64,6 +64,10 @@ enum frnn_flags {
    * to the same interval before adding the caller's cotangent
    * (fused/lstm_fused_pointwise.cuh:76-80, 115-124). */
   FRNN_GRAD_CLIP = 8,
+  /* Tests of failure handling only: every exchange poll waits for a tag that is never
+   * written, so each wait ends at the spin limit (frnn_set_spin_limit) with FRNN_E_TIMEOUT
+   * and every wave leaves its loop. */
+  FRNN_TEST_UNREADY = 16,
 };
 
 typedef struct frnn_desc {
@@ -140,7 +144,7 @@ int frnn_timing_read(double* ms3, int32_t* counts3);
  * [4] exchange polls, [5] steps, [6] backward partial-sum reduction. I/O
  * waves: [0] ring fill, [1] load issue, [2] barrier, [3] output drain,
  * [5] steps. Every wave of workgroups 0-127 also writes a timeline of steps
- * 64-79 (four 100 MHz clock stamps per step, 64 words per wave) at word
+ * 64-71 (eight 100 MHz clock stamps per step, 64 words per wave) at word
  * 256 + (workgroup * 16 + wave) * 64 (forward) and 131328 + the same
  * (backward); the buffer then needs 262400 words. NULL disables. */
 void frnn_set_phase_profile(void* device_words);

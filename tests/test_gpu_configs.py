@@ -164,18 +164,26 @@ def test_c5_chunked_equals_unchunked():
 
 
 def test_spin_limit_reports_timeout():
+    """Forced from the host: every poll waits for a tag that is never written
+    (FRNN_TEST_UNREADY) and gives up after one poll; the call reports
+    FRNN_E_TIMEOUT and every wave exits."""
+    import sys
+
     from flashrnn_amd import _lib, flashrnn
 
-    print("\n[timeout] spin limit 1", flush=True)
+    F = sys.modules["flashrnn_amd.flashrnn"]
+    print("\n[timeout] never-ready exchange, spin limit 1", flush=True)
     cpu, dh, dl = bf16_inputs("lstm", 4, 64, 2, 128, seed=6)
     lib = _lib.load()
     gl = [t.to("cuda", torch.bfloat16) for t in cpu]
     lib.frnn_set_spin_limit(1)
+    F._state["test_unready"] = True
     try:
         with pytest.raises(RuntimeError, match="code -5"):
             flashrnn(*gl, function="lstm", dtype="bfloat16")
             torch.cuda.synchronize()
     finally:
+        F._state["test_unready"] = False
         lib.frnn_set_spin_limit(0)
     # the GPU is usable afterwards and results are right again
     check(gpu_run("lstm", cpu, dh, dl), oracle_run("lstm", cpu, dh, dl))
