@@ -139,8 +139,18 @@ int make_plan(const frnn_desc* d, Plan* p) {
   p->dt_io = d->dtype_io;
   p->dt_state = d->dtype_state;
   p->flags = d->flags;
-  if (d->flags & ~(FRNN_TRAINING | FRNN_XCD_SHARED | FRNN_GRAD_CUT | FRNN_GRAD_CLIP | FRNN_TEST_UNREADY))
+  if (d->flags & ~(FRNN_TRAINING | FRNN_XCD_SHARED | FRNN_GRAD_CUT | FRNN_GRAD_CLIP | FRNN_TEST_UNREADY |
+                   FRNN_OUT_HIDDEN | FRNN_OUT_LAST | FRNN_SNAPSHOT_F32))
     return FRNN_E_INVALID;
+  if ((d->flags & FRNN_OUT_HIDDEN) && (d->flags & FRNN_OUT_LAST)) return FRNN_E_INVALID;
+  p->Ttot = d->total_steps == 0 ? d->steps : d->total_steps;
+  p->t0 = d->step_base;
+  if (p->t0 < 0 || p->Ttot < 1 || (long long)p->t0 + d->steps > p->Ttot) return FRNN_E_INVALID;
+  p->dt_out = (d->flags & FRNN_SNAPSHOT_F32) ? FRNN_F32 : d->dtype_io;
+  // the backward reads the full state history of the whole sequence
+  if ((d->flags & FRNN_TRAINING) &&
+      ((d->flags & (FRNN_OUT_HIDDEN | FRNN_OUT_LAST | FRNN_SNAPSHOT_F32)) || p->Ttot != d->steps))
+    return FRNN_E_UNSUPPORTED;
   if (d->flags & FRNN_GRAD_CLIP) {
     if (!(d->clipval >= 0.f) || d->clipval > 3.4e38f) return FRNN_E_INVALID;  // NaN, negative or infinite
     p->clip = d->clipval;
@@ -195,8 +205,11 @@ int make_plan(const frnn_desc* d, Plan* p) {
   p->save_bytes = align_up(p->save_floats * 4);
   // workspaces: status word at 0, exchange at 256
   p->off_x = kAlign;
-  p->ws_fwd = align_up(p->off_x + 2 * p->xwords_fwd * wsz);
-  p->off_dcand = align_up(p->off_x + 2 * p->xwords_bwd * wsz);
+  const long long nclaim = (long long)p->ngroups * frnn::kXcds * 4;  // by a launch's first group
+  p->off_claim_f = align_up(p->off_x + 2 * p->xwords_fwd * wsz);
+  p->ws_fwd = align_up(p->off_claim_f + nclaim);
+  p->off_claim_b = align_up(p->off_x + 2 * p->xwords_bwd * wsz);
+  p->off_dcand = align_up(p->off_claim_b + nclaim);
   const long long ndcand = p->cell == FRNN_GRU ? (long long)p->B * p->T * p->N * p->D : 0;
   p->off_part = align_up(p->off_dcand + ndcand * 4);
   p->off_dbpart = align_up(p->off_part + (long long)p->splitk * p->N * p->GR * p->D * p->D * 4);
@@ -314,8 +327,8 @@ int frnn_fwd(const frnn_desc* d, const void* wx, const void* R, const void* b, c
   if (!fn) return FRNN_E_UNSUPPORTED;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   char* w = static_cast<char*>(ws);
-  const long long xbytes = p.ws_fwd - p.off_x;
-  if ((rc = clear(w + p.off_x, xbytes, st)) != FRNN_OK) return rc;
+  const long long xbytes = 2 * p.xwords_fwd * (p.mma == FRNN_MMA_BF16 ? 4 : 8);
+  if ((rc = clear(w + p.off_x, p.ws_fwd - p.off_x, st)) != FRNN_OK) return rc;  // exchange and claims
   frnn::FwdArgs a;
   a.p = p;
   a.wx = wx;
@@ -327,6 +340,7 @@ int frnn_fwd(const frnn_desc* d, const void* wx, const void* R, const void* b, c
   a.save = training ? static_cast<float*>(save) : nullptr;
   a.xbuf = w + p.off_x;
   a.xbytes = xbytes;
+  a.claim = reinterpret_cast<uint32_t*>(w + p.off_claim_f);
   a.status = reinterpret_cast<uint32_t*>(w);
   a.spin_limit = g_spin_limit.load();
   a.prof = g_phase_prof.load();
@@ -349,14 +363,16 @@ int frnn_bwd(const frnn_desc* d, const void* R, const void* s0, const void* stat
   int rc = make_plan(d, &p);
   if (rc != FRNN_OK) return rc;
   if (!R || !s0 || !states || !save || !dwx || !dR || !db || !ds0 || !ws) return FRNN_E_INVALID;
+  if ((p.flags & (FRNN_OUT_HIDDEN | FRNN_OUT_LAST | FRNN_SNAPSHOT_F32)) || p.Ttot != p.T || p.t0 != 0)
+    return FRNN_E_INVALID;  // forward-only options
   if ((long long)ws_bytes < p.ws_bwd) return FRNN_E_WORKSPACE;
   const void* fn =
       frnn::recurrence_kernel(p.cell, p.mma, p.KSB, ktw_class((p.kt_fwd + p.KSB - 1) / p.KSB, p.NDT), p.NDT, false);
   if (!fn) return FRNN_E_UNSUPPORTED;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   char* w = static_cast<char*>(ws);
-  const long long xbytes = p.off_dcand - p.off_x;
-  if ((rc = clear(w + p.off_x, xbytes, st)) != FRNN_OK) return rc;
+  const long long xbytes = 2 * p.xwords_bwd * (p.mma == FRNN_MMA_BF16 ? 4 : 8);
+  if ((rc = clear(w + p.off_x, p.off_dcand - p.off_x, st)) != FRNN_OK) return rc;  // exchange and claims
   frnn::BwdArgs a;
   a.p = p;
   a.R = R;
@@ -369,6 +385,7 @@ int frnn_bwd(const frnn_desc* d, const void* R, const void* s0, const void* stat
   a.dbpart = reinterpret_cast<float*>(w + p.off_dbpart);
   a.xbuf = w + p.off_x;
   a.xbytes = xbytes;
+  a.claim = reinterpret_cast<uint32_t*>(w + p.off_claim_b);
   a.status = reinterpret_cast<uint32_t*>(w);
   a.spin_limit = g_spin_limit.load();
   a.prof = g_phase_prof.load();

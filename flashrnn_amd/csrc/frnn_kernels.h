@@ -18,6 +18,7 @@ struct FwdArgs {
   float* save;              // lane-native saved values (training) or null
   char* xbuf;               // exchange, both parities
   long long xbytes;
+  uint32_t* claim;          // zeroed slot counters (XCD-local exchange)
   uint32_t* status;
   uint32_t spin_limit;
   unsigned long long* prof;  // phase profile (8 words) or null
@@ -35,6 +36,7 @@ struct BwdArgs {
   float* dbpart;
   char* xbuf;
   long long xbytes;
+  uint32_t* claim;          // zeroed slot counters (XCD-local exchange)
   uint32_t* status;
   uint32_t spin_limit;
   unsigned long long* prof;  // phase profile (8 words, after the forward's 8) or null

@@ -18,12 +18,16 @@ constexpr int kMaxKT = 8;     // max 32-wide k-tiles per gate and wave (forward)
 constexpr int kMaxNFB = 32;   // max 32-wide k-tiles per wave (backward)
 // Plan flags (the C ABI's frnn_flags)
 constexpr int kFlagTraining = 1, kFlagShared = 2, kFlagCut = 4, kFlagClip = 8, kFlagUnready = 16;
+constexpr int kFlagOutHidden = 32, kFlagOutLast = 64, kFlagSnapF32 = 128;
 
 struct Plan {
   int cell, B, T, N, D;
   int GR, GW, GT, S;
   int mma, dt_io, dt_state, flags;
   float clip;      // kFlagClip: clamp bound of h and of its recurrent cotangent
+  int Ttot, t0;    // forward step window: Wx and the outputs hold Ttot steps, this call runs
+                   // steps [t0, t0 + T) of them (Ttot == T, t0 == 0 for a whole sequence)
+  int dt_out;      // dtype of the state output (dt_io, or FP32 with kFlagSnapF32)
   int NB;          // 16-row batch tiles per group
   int BS;          // slab rows = 16 * NB
   int nslab;       // ceil(B / BS)
@@ -47,23 +51,26 @@ struct Plan {
   long long ws_fwd, ws_bwd, save_bytes;
   long long off_dcand;                // backward workspace: GRU candidate-gate cotangents
   long long off_x, off_flag;          // workspace offsets (status word at 0)
+  long long off_claim_f, off_claim_b; // workgroup slot counters: 8 per launch (one per XCD), by first group
   long long off_part, off_dbpart;     // backward: dR split-K partials, db partials
 };
 
 // Group / tile of a workgroup; returns false for an idle workgroup.
+//  * placement-free exchange: workgroup index wg in a compact grid;
+//  * XCD-local exchange: wg is the workgroup's claim on its XCD (the
+//    workgroups that run on XCD x number themselves 0, 1, ... in arrival
+//    order), and groups x, x + 8, x + 16, ... of the launch live on XCD x.
 #if defined(__HIPCC__)
 __host__ __device__
 #endif
-inline bool wg_decode(const Plan& p, int wg, int* group, int* member) {
+inline bool wg_decode(const Plan& p, int wg, int xcd, int* group, int* member) {
   int local;
-  if (p.flags & 2) {  // placement-free exchange: compact grid
+  if (p.flags & 2) {
     local = wg / p.wpg;
     *member = wg % p.wpg;
   } else {
-    const int xcd = wg % kXcds;
-    const int idx = wg / kXcds;
-    const int slot = idx / p.wpg;
-    *member = idx % p.wpg;
+    const int slot = wg / p.wpg;
+    *member = wg % p.wpg;
     local = slot * kXcds + xcd;
   }
   *group = p.g0 + local;

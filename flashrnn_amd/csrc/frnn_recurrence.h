@@ -90,12 +90,34 @@ struct Team {
   int group, member, n, slab, dt, wgi;
 };
 
-__device__ __forceinline__ bool team_setup(const Plan& p, Team& tm, uint32_t* status, int KS) {
-  if (!wg_decode(p, blockIdx.x, &tm.group, &tm.member)) return false;
-  if (!(p.flags & 2) && xcc_id() != (uint32_t)(blockIdx.x % kXcds)) {
-    if (threadIdx.x == 0) raise_status(status, ST_PLACEMENT);
-    return false;  // the whole workgroup leaves together; partners time out or see the status
+// XCD-local exchange: the workgroup claims the next free slot of the XCD it
+// runs on (read from the hardware), so every group is XCD-local whatever order
+// the dispatcher hands workgroups to XCDs in. A launch's grid holds the same
+// number of slots on every XCD; a workgroup beyond them (an uneven dispatch)
+// raises the placement status and leaves, and its partners time out.
+// The claim is broadcast through the first word of the kernel's dynamic LDS
+// (a static __shared__ variable would shift the dynamic area off its 16-byte
+// alignment), which is free again after the second barrier.
+__device__ __forceinline__ bool team_setup(const Plan& p, Team& tm, uint32_t* claim, uint32_t* status, int KS,
+                                           float* lds) {
+  int wg = blockIdx.x, xcd = 0;
+  if (!(p.flags & 2)) {
+    volatile uint32_t* s_slot = reinterpret_cast<volatile uint32_t*>(lds);
+    xcd = (int)(xcc_id() & 15u);
+    if (threadIdx.x == 0)
+      *s_slot = xcd < kXcds ? __hip_atomic_fetch_add(claim + (long)p.g0 * kXcds + xcd, 1u, __ATOMIC_RELAXED,
+                                                     __HIP_MEMORY_SCOPE_AGENT)
+                            : 0xffffffffu;
+    __syncthreads();
+    const uint32_t slot = *s_slot;
+    __syncthreads();
+    if (slot >= (uint32_t)(p.grid / kXcds)) {
+      if (threadIdx.x == 0) raise_status(status, ST_PLACEMENT);
+      return false;  // the whole workgroup leaves together
+    }
+    wg = (int)slot;
   }
+  if (!wg_decode(p, wg, xcd, &tm.group, &tm.member)) return false;
   tm.lane = threadIdx.x & 63;
   tm.w = threadIdx.x >> 6;
   tm.team = tm.w / (KS + 1);
@@ -416,14 +438,17 @@ __device__ void fwd_io(const FwdArgs& a, const Team& tm, float* xring, float* os
   constexpr int GW = CS::GW, S = CS::S, NE = NB * 256, P = kFwdAhead;
   constexpr int NSAVE = Cell<CELL>::NSAVE, NV = Lds<CELL, NB>::NV, RING = Lds<CELL, NB>::RING;
   const Plan& p = a.p;
-  const int T = p.T, N = p.N, D = p.D, B = p.B;
+  const int T = p.T, N = p.N, D = p.D, B = p.B, TT = p.Ttot, t0 = p.t0;
   const bool training = (p.flags & 1) != 0;
+  // output policy: all S states, the hidden state only, or the sequence's last hidden state only
+  const int mode = (p.flags & kFlagOutLast) ? 2 : ((p.flags & kFlagOutHidden) ? 1 : 0);
+  const int nst = mode == 0 ? S : 1;
   const long wx_t = (long)GW * N * D;
   // loads: lane -> (row, quad); BF16 chunks hold 8 units, so odd quads idle
   const int lrow = tm.lane >> 2, lquad = tm.lane & 3;
   const int lb = tm.slab * p.BS + lrow;
   const bool lval = lb < B && (p.dt_io == DT_F32 || (lquad & 1) == 0);
-  const long lbase = ((long)lb * T) * wx_t + (long)tm.n * D + tm.dt * 16 + 4 * lquad;
+  const long lbase = ((long)lb * TT + t0) * wx_t + (long)tm.n * D + tm.dt * 16 + 4 * lquad;
   const int esz = p.dt_io == DT_F32 ? 4 : 2;
   auto load_wx = [&](int u) {
     float* slot = xring + (long)(u % kFwdRing) * RING;
@@ -438,13 +463,18 @@ __device__ void fwd_io(const FwdArgs& a, const Team& tm, float* xring, float* os
   const int e0 = io_elem(tm.lane, 0);
   const Elem el = elem_of(p, tm, e0);
   auto store_out = [&](int t, const float* src) {
+    if (mode == 2) {  // [B,1,N,D]: the last step of the sequence only
+      if (t0 + t == TT - 1 && el.real)
+        st4(a.states, ((long)el.b * N + tm.n) * D + el.d, p.dt_out, *reinterpret_cast<const f32x4*>(src + e0));
+      return;
+    }
 #pragma unroll
     for (int v = 0; v < NV; ++v) {
-      if (v >= S && !training) break;
+      if (v >= nst && !training) break;
       const f32x4 x = *reinterpret_cast<const f32x4*>(src + v * NE + e0);
       if (!el.real) continue;
       if (v < S)
-        st4(a.states, ((((long)v * B + el.b) * T + t) * N + tm.n) * D + el.d, p.dt_io, x);
+        st4(a.states, ((((long)v * B + el.b) * TT + t0 + t) * N + tm.n) * D + el.d, p.dt_out, x);
       else
         *reinterpret_cast<f32x4*>(a.save + save_index(p, NE, t, tm.wgi, v - S, tm.team, e0)) = x;
     }
@@ -454,7 +484,8 @@ __device__ void fwd_io(const FwdArgs& a, const Team& tm, float* xring, float* os
   // of step t+1, at the top of iteration t (steady state): P-2 iterations of
   // stores and loads.
   static_assert(P >= 2, "prefetch distance");
-  constexpr int kAfterTrain = (P - 2) * (GW + NV), kAfterInfer = (P - 2) * (GW + S);
+  constexpr int kAfterTrain = (P - 2) * (GW + NV), kAfterFull = (P - 2) * (GW + S);
+  constexpr int kAfterHidden = (P - 2) * (GW + 1), kAfterLast = (P - 2) * GW;
 
   Prof prof;
   prof.init(a.prof != nullptr && blockIdx.x == 0, a.prof != nullptr);
@@ -464,7 +495,9 @@ __device__ void fwd_io(const FwdArgs& a, const Team& tm, float* xring, float* os
   for (int t = 0; t < T; ++t) {
     if (t + 1 >= P && t + P <= T) {
       if (training) wait_vm<kAfterTrain>();
-      else wait_vm<kAfterInfer>();
+      else if (mode == 0) wait_vm<kAfterFull>();
+      else if (mode == 1) wait_vm<kAfterHidden>();
+      else wait_vm<kAfterLast>();
     } else {
       wait_vm<0>();
     }
@@ -496,23 +529,26 @@ __global__ void __launch_bounds__(64 * (KSC + 1) * NDT) fwd_kernel(FwdArgs a) {
   constexpr int NE = NB * 256, EPLMAX = (4 * NB + KSC - 1) / KSC, KS = KSC;
   constexpr int NSAVE = Cell<CELL>::NSAVE, NV = Lds<CELL, NB>::NV, RING = Lds<CELL, NB>::RING;
   const Plan& p = a.p;
+  extern __shared__ float lds[];
   Team tm;
-  if (!team_setup(p, tm, a.status, KSC)) return;
+  if (!team_setup(p, tm, a.claim, a.status, KSC, lds)) return;
   const int D = p.D, B = p.B, T = p.T, N = p.N;
 
-  extern __shared__ float lds[];
   constexpr int RED_F = Lds<CELL, NB>::RED_F;
   float* red = lds + tm.team * Lds<CELL, NB>::fwd(KS);  // [2][KS][NB][272][4]
   float* xring = red + 2L * KS * NB * RED_F;            // [slot][gate][64][4]
   float* ost = xring + (long)kFwdRing * RING;           // [2][NV][NE]
 
-  // sLSTM: the reference's global predicate all(n0 == 0) over the call's whole initial state
+  // sLSTM: the reference's global predicate all(n0 == 0) over the call's whole initial state,
+  // at the first step of a sequence only (a later window continues from a carry)
   uint32_t zflag = 0;
   if constexpr (CELL == CELL_SLSTM) {
-    int nz = 0;
-    const long cnt = (long)B * N * D;
-    for (long i = threadIdx.x; i < cnt; i += blockDim.x) nz |= ld_val(a.s0, 2 * cnt + i, p.dt_state) != 0.f;
-    zflag = __syncthreads_or(nz) ? 0u : 1u;
+    if (p.t0 == 0) {
+      int nz = 0;
+      const long cnt = (long)B * N * D;
+      for (long i = threadIdx.x; i < cnt; i += blockDim.x) nz |= ld_val(a.s0, 2 * cnt + i, p.dt_state) != 0.f;
+      zflag = __syncthreads_or(nz) ? 0u : 1u;
+    }
   }
   if (tm.kw == KS) {
     fwd_io<CELL, MMA, NB>(a, tm, xring, ost);
@@ -827,13 +863,13 @@ __global__ void __launch_bounds__(64 * (KSC + 1) * NDT) bwd_kernel(BwdArgs a) {
   constexpr int NOP = Lds<CELL, NB>::NOP, NOB = Lds<CELL, NB>::NOB;
   constexpr int NF = GR * KTW;  // max fragments of R^T per wave
   const Plan& p = a.p;
+  extern __shared__ float lds[];
   Team tm;
-  if (!team_setup(p, tm, a.status, KSC)) return;
+  if (!team_setup(p, tm, a.claim, a.status, KSC, lds)) return;
   const int D = p.D, B = p.B, N = p.N, T = p.T;
   const int GD = GR * D;
   const bool cut = (p.flags & kFlagCut) != 0;
 
-  extern __shared__ float lds[];
   constexpr int RED_B = Lds<CELL, NB>::RED_B;
   float* red = lds + tm.team * Lds<CELL, NB>::bwd(KS);  // [2][NB][KS][304]
   float* iring = red + 2L * NB * KS * RED_B;             // [P][NE][NOP]

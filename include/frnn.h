@@ -68,6 +68,15 @@ enum frnn_flags {
    * written, so each wait ends at the spin limit (frnn_set_spin_limit) with FRNN_E_TIMEOUT
    * and every wave leaves its loop. */
   FRNN_TEST_UNREADY = 16,
+  /* Forward-only output policies of FlashRNN2's prepared execution
+   * (flashrnn/flashrnn2/prepared.py:18-71, triton_persistent.py:154-166); not with
+   * FRNN_TRAINING. FRNN_OUT_HIDDEN: states_out is the hidden-state history only,
+   * [B,T,N,D]. FRNN_OUT_LAST: states_out is the hidden state of the sequence's last
+   * step only, [B,1,N,D], written by the call whose window ends the sequence.
+   * FRNN_SNAPSHOT_F32: states_out is FP32 instead of dtype_io. */
+  FRNN_OUT_HIDDEN = 32,
+  FRNN_OUT_LAST = 64,
+  FRNN_SNAPSHOT_F32 = 128,
 };
 
 typedef struct frnn_desc {
@@ -81,6 +90,14 @@ typedef struct frnn_desc {
   int32_t mma;         /* enum frnn_mma */
   int32_t flags;       /* enum frnn_flags */
   float clipval;       /* with FRNN_GRAD_CLIP: finite and >= 0; otherwise ignored */
+  /* Forward step window (FlashRNN2's chunked prepared execution, prepared.py:114-162):
+   * Wx and states_out hold total_steps steps, and the call runs steps
+   * [step_base, step_base + steps) of them from s0, writing those steps of
+   * states_out in place. total_steps == 0 means steps. The sLSTM zero-normalizer
+   * predicate applies only at step 0 of the sequence (step_base == 0). Not with
+   * FRNN_TRAINING (the backward needs a whole sequence). */
+  int32_t total_steps;
+  int32_t step_base;
 } frnn_desc;
 
 enum frnn_status {
