@@ -88,12 +88,81 @@ def cpu_baseline(torch, budget_s=30.0):
     }
 
 
+def _time_ms(torch, fn, reps=20, warmup=3):
+    """Median milliseconds of fn() over reps, each bracketed by device synchronisation."""
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        fn()
+        torch.cuda.synchronize()
+        times.append((time.perf_counter() - t0) * 1e3)
+    times.sort()
+    return round(times[len(times) // 2], 4)
+
+
+def extras(torch, dev, flashrnn):
+    """Side measurements, not the metric:
+    * the shape of the reference's only published timing of this path (v1
+      cuda_fused LSTM, B16 T1024 N3 D256 bf16, H100 SXM: forward 3.62 ms,
+      forward+backward 11.3 ms; README speed figure head_dim--lstm.svg);
+    * FlashRNN2's prepared inference (forward only, hidden-state output,
+      captured HIP graph) at the metric's shape B8 T1024 N3 D256.
+    Inputs are seeded normals as in make_inputs."""
+    from flashrnn_amd.prepared import PreparedSequence
+
+    out = {}
+    g = torch.Generator().manual_seed(7)
+    Bp = 16
+    wx = torch.randn(Bp, T, G, N, D, generator=g).to(dev, torch.bfloat16).requires_grad_()
+    R = (torch.randn(G, N, D, D, generator=g) / D**0.5).to(dev, torch.bfloat16).requires_grad_()
+    b = (0.1 * torch.randn(G, N, D, generator=g)).to(dev, torch.bfloat16).requires_grad_()
+    s0 = torch.zeros(S, Bp, 1, N, D, device=dev, dtype=torch.bfloat16, requires_grad=True)
+    dh = torch.randn(S, Bp, T, N, D, generator=g).to(dev, torch.bfloat16)
+    dl = torch.randn(S, Bp, 1, N, D, generator=g).to(dev, torch.bfloat16)
+
+    def fwd():
+        with torch.no_grad():
+            flashrnn(wx, R, b, s0, function="lstm", dtype="bfloat16")
+
+    def fwdbwd():
+        h, last = flashrnn(wx, R, b, s0, function="lstm", dtype="bfloat16")
+        torch.autograd.grad((h, last), (wx, R, b, s0), grad_outputs=(dh, dl))
+
+    f_ms, fb_ms = _time_ms(torch, fwd), _time_ms(torch, fwdbwd)
+    out["reference_published_shape"] = {
+        "workload": "LSTM B16 T1024 N3 D256 bf16",
+        "fwd_ms": f_ms, "fwd_bwd_ms": fb_ms,
+        "h100_cuda_fused_fwd_ms": 3.62, "h100_cuda_fused_fwd_bwd_ms": 11.3,
+        "speedup_fwd": round(3.62 / f_ms, 2), "speedup_fwd_bwd": round(11.3 / fb_ms, 2),
+    }
+    x = torch.randn(B, T, G, N, D, generator=g).to(dev, torch.bfloat16)
+    Rp = (torch.randn(G, N, D, D, generator=g) / D**0.5).to(dev, torch.bfloat16)
+    bp = (0.1 * torch.randn(G, N, D, generator=g)).to(dev, torch.bfloat16)
+    init = torch.zeros(S, B, 1, N, D, device=dev)
+    p = PreparedSequence(x, Rp, bp, init, "lstm", output_mode="hidden").capture()
+    try:
+        ms = _time_ms(torch, p.run)
+        p.check()
+    finally:
+        p.close()
+    out["prepared_inference"] = {
+        "workload": "LSTM B8 T1024 N3 D256 bf16, forward only, hidden output, HIP graph",
+        "ms": ms, "timesteps_batch_per_s": round(B * T / (ms / 1e3), 1),
+    }
+    return out
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=30)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-extras", action="store_true",
+                    help="skip the side measurements (reference-published shape, prepared inference)")
     ap.add_argument("--phases", action="store_true", help="also report the in-kernel phase profile")
     ap.add_argument("--trace-out", default=None, help="with --phases: save the per-wave step timelines "
                     "[fwd/bwd][workgroup][wave][step][stamp] (100 MHz clock) as .npy")
@@ -215,6 +284,8 @@ def main(argv=None):
         if args.trace_out:
             import numpy as np
             np.save(args.trace_out, np.array(v[256:], dtype=np.int64).reshape(2, 128, 16, 8, 8))
+    if not args.no_extras:
+        result["extras"] = extras(torch, dev, flashrnn)
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(torch)
     print(json.dumps(result), flush=True)

@@ -17,7 +17,7 @@ FRNN_LSTM, FRNN_GRU, FRNN_ELMAN, FRNN_SLSTM = 0, 1, 2, 3
 FRNN_F32, FRNN_BF16 = 0, 1
 FRNN_MMA_BF16, FRNN_MMA_F32 = 0, 1
 FRNN_TRAINING, FRNN_XCD_SHARED, FRNN_GRAD_CUT, FRNN_GRAD_CLIP, FRNN_TEST_UNREADY = 1, 2, 4, 8, 16
-FRNN_OUT_HIDDEN, FRNN_OUT_LAST, FRNN_SNAPSHOT_F32 = 32, 64, 128
+FRNN_OUT_HIDDEN, FRNN_OUT_LAST, FRNN_SNAPSHOT_F32, FRNN_SLSTM_V1GRAD = 32, 64, 128, 256
 FRNN_OK = 0
 FRNN_E_TIMEOUT = -5
 FRNN_E_PLACEMENT = -6

@@ -140,17 +140,15 @@ int make_plan(const frnn_desc* d, Plan* p) {
   p->dt_state = d->dtype_state;
   p->flags = d->flags;
   if (d->flags & ~(FRNN_TRAINING | FRNN_XCD_SHARED | FRNN_GRAD_CUT | FRNN_GRAD_CLIP | FRNN_TEST_UNREADY |
-                   FRNN_OUT_HIDDEN | FRNN_OUT_LAST | FRNN_SNAPSHOT_F32))
+                   FRNN_OUT_HIDDEN | FRNN_OUT_LAST | FRNN_SNAPSHOT_F32 | FRNN_SLSTM_V1GRAD))
     return FRNN_E_INVALID;
   if ((d->flags & FRNN_OUT_HIDDEN) && (d->flags & FRNN_OUT_LAST)) return FRNN_E_INVALID;
   p->Ttot = d->total_steps == 0 ? d->steps : d->total_steps;
   p->t0 = d->step_base;
   if (p->t0 < 0 || p->Ttot < 1 || (long long)p->t0 + d->steps > p->Ttot) return FRNN_E_INVALID;
   p->dt_out = (d->flags & FRNN_SNAPSHOT_F32) ? FRNN_F32 : d->dtype_io;
-  // the backward reads the full state history of the whole sequence
-  if ((d->flags & FRNN_TRAINING) &&
-      ((d->flags & (FRNN_OUT_HIDDEN | FRNN_OUT_LAST | FRNN_SNAPSHOT_F32)) || p->Ttot != d->steps))
-    return FRNN_E_UNSUPPORTED;
+  // the backward needs the hidden-state history of the whole sequence (its dR GEMM operand)
+  if ((d->flags & FRNN_TRAINING) && ((d->flags & FRNN_OUT_LAST) || p->Ttot != d->steps)) return FRNN_E_UNSUPPORTED;
   if (d->flags & FRNN_GRAD_CLIP) {
     if (!(d->clipval >= 0.f) || d->clipval > 3.4e38f) return FRNN_E_INVALID;  // NaN, negative or infinite
     p->clip = d->clipval;
@@ -363,8 +361,7 @@ int frnn_bwd(const frnn_desc* d, const void* R, const void* s0, const void* stat
   int rc = make_plan(d, &p);
   if (rc != FRNN_OK) return rc;
   if (!R || !s0 || !states || !save || !dwx || !dR || !db || !ds0 || !ws) return FRNN_E_INVALID;
-  if ((p.flags & (FRNN_OUT_HIDDEN | FRNN_OUT_LAST | FRNN_SNAPSHOT_F32)) || p.Ttot != p.T || p.t0 != 0)
-    return FRNN_E_INVALID;  // forward-only options
+  if ((p.flags & FRNN_OUT_LAST) || p.Ttot != p.T || p.t0 != 0) return FRNN_E_INVALID;  // forward-only options
   if ((long long)ws_bytes < p.ws_bwd) return FRNN_E_WORKSPACE;
   const void* fn =
       frnn::recurrence_kernel(p.cell, p.mma, p.KSB, ktw_class((p.kt_fwd + p.KSB - 1) / p.KSB, p.NDT), p.NDT, false);

@@ -35,7 +35,7 @@ template <> struct Cell<CELL_LSTM> {
   // ds: total cotangents of (h_t, c_t). Out: dry (= dWx), cotangent carried to
   // (h_{t-1}, c_{t-1}) through direct (non-recurrent) paths.
   __device__ __forceinline__ static void bwd(const float* ds, const float* sv, float* dry, float* dwx,
-                                             float* db, float* carry) {
+                                             float* db, float* carry, bool v1) {
     const float si = sv[0], sf = sv[1], tz = sv[2], so = sv[3], tc = sv[4], cp = sv[5];
     const float dh = ds[0];
     const float dc = ds[1] + dh * so * (1.f - tc * tc);
@@ -65,7 +65,7 @@ template <> struct Cell<CELL_GRU> {
     st[0] = u * st[0] + (1.f - u) * v;
   }
   __device__ __forceinline__ static void bwd(const float* ds, const float* sv, float* dry, float* dwx,
-                                             float* db, float* carry) {
+                                             float* db, float* carry, bool v1) {
     const float r = sv[0], u = sv[1], v = sv[2], cand = sv[3], hp = sv[4];
     const float dh = ds[0];
     const float dva = dh * (1.f - u) * (1.f - v * v);
@@ -87,7 +87,7 @@ template <> struct Cell<CELL_ELMAN> {
     sv[0] = st[0];
   }
   __device__ __forceinline__ static void bwd(const float* ds, const float* sv, float* dry, float* dwx,
-                                             float* db, float* carry) {
+                                             float* db, float* carry, bool v1) {
     const float h = sv[0];
     const float da = ds[0] * (1.f - h * h);
     dry[0] = da; dwx[0] = da; db[0] = da;
@@ -122,7 +122,7 @@ template <> struct Cell<CELL_SLSTM> {
     st[3] = m;
   }
   __device__ __forceinline__ static void bwd(const float* ds, const float* sv, float* dry, float* dwx,
-                                             float* db, float* carry) {
+                                             float* db, float* carry, bool v1) {
     const float so = sv[0], c = sv[1], nn = sv[2], tz = sv[3], ia = sv[4], fa = sv[5];
     const float cold = sv[6], nold = sv[7], sgn = sv[8], wn = sv[9], wm = sv[10];
     const float dh = ds[0];
@@ -130,15 +130,19 @@ template <> struct Cell<CELL_SLSTM> {
     const float dgo = dh * c * rn * so * (1.f - so);
     const float dc = ds[1] + dh * so * rn;
     const float dn = ds[2] - dh * so * c * rn * rn;
-    const float dnpre = dn * wn;
+    // v1 (FlashRNN v1 / FlashRNN2 training convention): the normalizer clamp passes
+    // its cotangent straight through and the stabilizer m carries none
+    const float dnpre = v1 ? dn : dn * wn;
     const float dfa = dc * cold + dnpre * nold;
     const float dia = dc * tz + dnpre;
     const float dgz = dc * ia * (1.f - tz * tz);
     float dgi = dia * ia;
     float dlf = dfa * fa;
-    const float dm = ds[3] - dia * ia - dfa * fa;
-    dgi += dm * wm;
-    dlf += dm * (1.f - wm);
+    if (!v1) {
+      const float dm = ds[3] - dia * ia - dfa * fa;
+      dgi += dm * wm;
+      dlf += dm * (1.f - wm);
+    }
     const float dgf = dlf * sgn;
     dry[0] = dgi; dry[1] = dgf; dry[2] = dgz; dry[3] = dgo;
 #pragma unroll
@@ -146,7 +150,7 @@ template <> struct Cell<CELL_SLSTM> {
     carry[0] = 0.f;
     carry[1] = dc * fa;
     carry[2] = dnpre * fa;
-    carry[3] = dlf;
+    carry[3] = v1 ? 0.f : dlf;
   }
 };
 

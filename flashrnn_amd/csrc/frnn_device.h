@@ -172,6 +172,10 @@ __device__ __forceinline__ Frag<MMA> frag_keep(bool keep, const Frag<MMA>& f) {
 
 // ------------------------------------------------------ exchange words
 // BF16 path: 32-bit word = (tag << 16) | bf16 bits.   F32 path: 64-bit word = (tag << 32) | f32 bits.
+// Split words (the BF16 path's backward, whose exchanged gate cotangents are not
+// rounded to BF16 by the reference's policy): 32-bit word = the FP32 value rounded
+// to 21 mantissa bits, with the tag in the two lowest bits; the reader splits it
+// into hi + lo BF16 operands (16 significant bits) and multiplies both.
 // Tags cycle 1,1,2,2,1,1,... so a slot (double-buffered by step parity)
 // never holds its own step's tag before the step is written, and the
 // zero-cleared buffer never matches.
@@ -187,12 +191,14 @@ struct Xchg {
   int shared_xcd;               // 1: stores write through to memory-side coherence (sc1)
 };
 
+__device__ __forceinline__ uint32_t split_word(float v, uint32_t tag) { return ((f2u(v) + 2u) & ~3u) | tag; }
+
 // Store one exchange word. Same-XCD mode uses a non-temporal store (it lands
 // in the shared L2); the placement-free mode uses an agent-scope store.
-template <int MMA>
+template <int MMA, bool SPLIT = false>
 __device__ __forceinline__ void xstore(const Xchg& x, long word, float v, uint32_t tag) {
   if constexpr (MMA == MMA_BF16) {
-    uint32_t w = (tag << 16) | bf16_bits(v);
+    uint32_t w = SPLIT ? split_word(v, tag) : ((tag << 16) | bf16_bits(v));
     uint32_t* p = reinterpret_cast<uint32_t*>(x.base) + word;
     if (x.shared_xcd) __hip_atomic_store(p, w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     else __builtin_nontemporal_store(w, p);
@@ -206,13 +212,13 @@ __device__ __forceinline__ void xstore(const Xchg& x, long word, float v, uint32
 
 // Store the NV exchange words of one element (its gates, contiguous) with one
 // vector store.
-template <int MMA, int NV>
+template <int MMA, int NV, bool SPLIT = false>
 __device__ __forceinline__ void xstore_vec(const Xchg& x, long word, const float* v, uint32_t tag) {
   if constexpr (MMA == MMA_BF16 && NV == 4) {
     typedef uint32_t vec_t __attribute__((ext_vector_type(NV)));
     vec_t w;
 #pragma unroll
-    for (int i = 0; i < NV; ++i) w[i] = (tag << 16) | bf16_bits(v[i]);
+    for (int i = 0; i < NV; ++i) w[i] = SPLIT ? split_word(v[i], tag) : ((tag << 16) | bf16_bits(v[i]));
     uint32_t* p = reinterpret_cast<uint32_t*>(x.base) + word;
     if (x.shared_xcd) {
 #pragma unroll
@@ -222,7 +228,7 @@ __device__ __forceinline__ void xstore_vec(const Xchg& x, long word, const float
     }
   } else {
 #pragma unroll
-    for (int i = 0; i < NV; ++i) xstore<MMA>(x, word + i, v[i], tag);
+    for (int i = 0; i < NV; ++i) xstore<MMA, SPLIT>(x, word + i, v[i], tag);
   }
 }
 
@@ -292,6 +298,65 @@ __device__ __forceinline__ bool xunpack(const Run<MMA>& r, uint32_t tag, Frag<MM
   }
   return ok;
 }
+
+// Split words (BF16 path only): check the tags of a run and unpack it into
+// hi and lo operand fragments: hi = the upper 16 bits of the word (the value
+// truncated to BF16), lo = the exact remainder rounded to BF16, so hi + lo is
+// the value to about 16 significant bits (the tag bits add < 2^-20 relative).
+// Per pair of words: one byte permute (hi), two masks and subtractions and one
+// packed conversion (lo); the tags of the 8 words are checked together: every
+// word's low two bits equal tag iff both their OR and their AND do.
+template <int MMA>
+__device__ __forceinline__ bool xunpack_split(const Run<MMA>& r, uint32_t tag, Frag<MMA>& hi, Frag<MMA>& lo) {
+  static_assert(MMA == MMA_BF16, "split words exist on the BF16 path only");
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+  typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+  u32x4_t hp, lp;
+  uint32_t orv = 0u, andv = ~0u;
+#pragma unroll
+  for (int q = 0; q < 2; ++q)
+#pragma unroll
+    for (int e = 0; e < 4; e += 2) {
+      const uint32_t w0 = r.q[q][e], w1 = r.q[q][e + 1];
+      hp[2 * q + e / 2] = __builtin_amdgcn_perm(w1, w0, 0x07060302u);
+      const float l0 = u2f(w0) - u2f(w0 & 0xffff0000u);
+      const float l1 = u2f(w1) - u2f(w1 & 0xffff0000u);
+      const bf16x2_t l = {(__bf16)l0, (__bf16)l1};
+      lp[2 * q + e / 2] = __builtin_bit_cast(uint32_t, l);
+      orv |= w0 | w1;
+      andv &= w0 & w1;
+    }
+  hi.v = __builtin_bit_cast(bf16x8, hp);
+  lo.v = __builtin_bit_cast(bf16x8, lp);
+  return ((orv & 3u) == tag) & ((andv & 3u) == tag);
+}
+
+// Unpack a run into the operand(s) of its product: one fragment, or with split
+// words the hi and lo fragments.
+template <int MMA, bool SPLIT>
+struct Operand {
+  Frag<MMA> hi, lo;
+  __device__ __forceinline__ bool unpack(const Run<MMA>& r, uint32_t tag) {
+    if constexpr (SPLIT) return xunpack_split<MMA>(r, tag, hi, lo);
+    else return xunpack<MMA>(r, tag, hi);
+  }
+  __device__ __forceinline__ void keep(bool k) {
+    hi = frag_keep<MMA>(k, hi);
+    if constexpr (SPLIT) lo = frag_keep<MMA>(k, lo);
+  }
+  __device__ __forceinline__ Operand rot8() const {
+    Operand o;
+    o.hi = frag_rot8(hi);
+    if constexpr (SPLIT) o.lo = frag_rot8(lo);
+    return o;
+  }
+  // p(frag, part) adds one product into the caller's accumulators (part 1: the lo operand)
+  template <typename P>
+  __device__ __forceinline__ void apply(P p) const {
+    p(hi, 0);
+    if constexpr (SPLIT) p(lo, 1);
+  }
+};
 
 __device__ __forceinline__ uint32_t load_status(const uint32_t* status) {
   return __hip_atomic_load(status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);

@@ -69,8 +69,8 @@ struct GemmSrc {
       vh[1] = ld4(a->s0, i + 4, p.dt_state);
     } else {
       const long i = ((b * p.T + t - 1) * p.N + n) * p.D + q;  // h_{t-1} = states[0][b][t-1]
-      vh[0] = ld4(a->states, i, p.dt_io);
-      vh[1] = ld4(a->states, i + 4, p.dt_io);
+      vh[0] = ld4(a->states, i, p.dt_out);
+      vh[1] = ld4(a->states, i + 4, p.dt_out);
     }
   }
 };

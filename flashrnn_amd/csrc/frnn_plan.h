@@ -18,7 +18,7 @@ constexpr int kMaxKT = 8;     // max 32-wide k-tiles per gate and wave (forward)
 constexpr int kMaxNFB = 32;   // max 32-wide k-tiles per wave (backward)
 // Plan flags (the C ABI's frnn_flags)
 constexpr int kFlagTraining = 1, kFlagShared = 2, kFlagCut = 4, kFlagClip = 8, kFlagUnready = 16;
-constexpr int kFlagOutHidden = 32, kFlagOutLast = 64, kFlagSnapF32 = 128;
+constexpr int kFlagOutHidden = 32, kFlagOutLast = 64, kFlagSnapF32 = 128, kFlagV1Grad = 256;
 
 struct Plan {
   int cell, B, T, N, D;

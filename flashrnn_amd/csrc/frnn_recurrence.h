@@ -225,10 +225,11 @@ template <int MMA, int NDT> struct PollChunk {
 // Ranges of more than PollChunk runs are polled in chunks: each chunk is
 // polled until all of its tags are fresh and only then multiplied, so a
 // stale chunk never has to be taken back out of the accumulators.
-template <int MMA, int NDT, int NB, int NF, typename Zero, typename Prod>
+template <int MMA, int NDT, int NB, int NF, bool SPLIT = false, typename Zero, typename Prod>
 __device__ __forceinline__ uint32_t gather_mma(const Xchg& x, const int (&word)[NB][NF], const bool (&bval)[NB],
                                                int off, int cstride, int nf, uint32_t tag, uint32_t* status, uint32_t spin_limit,
                                                bool& abort, Zero zero, Prod prod) {
+  using Op = Operand<MMA, SPLIT>;
   uint32_t spins = 0;
   if constexpr (NF <= PollChunk<MMA, NDT>::value) {
     while (true) {
@@ -250,10 +251,11 @@ __device__ __forceinline__ uint32_t gather_mma(const Xchg& x, const int (&word)[
 #pragma unroll
         for (int j = 0; j < NF; ++j)
           if (j < nf) {
-            Frag<MMA> f;
-            const bool fresh = xunpack<MMA>(r[bt][j], tag, f);
+            Op o;
+            const bool fresh = o.unpack(r[bt][j], tag);
             ok &= fresh || !bval[bt];
-            prod(bt, j, frag_keep<MMA>(bval[bt], f));
+            o.keep(bval[bt]);
+            o.apply([&](const Frag<MMA>& f, int part) { prod(bt, j, f, part); });
           }
       ++spins;
       if (__all(ok)) return spins;
@@ -286,8 +288,8 @@ __device__ __forceinline__ uint32_t gather_mma(const Xchg& x, const int (&word)[
 #pragma unroll
           for (int jj = 0; jj < CH; ++jj)
             if (c0 + jj < NF && c0 + jj < nf) {
-              Frag<MMA> f;
-              ok &= xunpack<MMA>(r[bt][jj], tag, f) || !bval[bt];
+              Op o;
+              ok &= o.unpack(r[bt][jj], tag) || !bval[bt];
             }
         ++spins;
         if (__all(ok)) {
@@ -296,9 +298,10 @@ __device__ __forceinline__ uint32_t gather_mma(const Xchg& x, const int (&word)[
 #pragma unroll
             for (int jj = 0; jj < CH; ++jj)
               if (c0 + jj < NF && c0 + jj < nf) {
-                Frag<MMA> f;
-                xunpack<MMA>(r[bt][jj], tag, f);
-                prod(bt, c0 + jj, frag_keep<MMA>(bval[bt], f));
+                Op o;
+                o.unpack(r[bt][jj], tag);
+                o.keep(bval[bt]);
+                o.apply([&](const Frag<MMA>& f, int part) { prod(bt, c0 + jj, f, part); });
               }
           break;
         }
@@ -320,13 +323,25 @@ __device__ __forceinline__ uint32_t gather_mma(const Xchg& x, const int (&word)[
 // half the loads; the odd tile then moves down 8 lanes (DPP) and the upper
 // lanes contribute zero. word[j] is the run of k-tile j for batch row lane % 8.
 // Long ranges are polled in chunks of PollChunk pairs, as in gather_mma.
-template <int MMA, int NDT, int NF, typename Zero, typename Prod>
+template <int MMA, int NDT, int NF, bool SPLIT = false, typename Zero, typename Prod>
 __device__ __forceinline__ uint32_t gather_pair_mma(const Xchg& x, const int (&word)[NF], bool bv, int off, int cstride, int nf,
                                                     uint32_t tag, uint32_t* status, uint32_t spin_limit, bool& abort,
                                                     Zero zero, Prod prod) {
+  using Op = Operand<MMA, SPLIT>;
   constexpr int NP = (NF + 1) / 2;
   constexpr int CH = NP <= PollChunk<MMA, NDT>::value ? NP : PollChunk<MMA, NDT>::value;
   const int hi = (threadIdx.x >> 3) & 1;  // lane % 16 >= 8
+  // the pair's products: the even tile in place, the odd one moved down 8 lanes
+  auto pair_prod = [&](Op o, int i) {
+    const Op odd = o.rot8();
+    o.keep(!hi);
+    o.apply([&](const Frag<MMA>& f, int part) { prod(0, 2 * i, f, part); });
+    if (2 * i + 1 < nf) {
+      Op od = odd;
+      od.keep(!hi);
+      od.apply([&](const Frag<MMA>& f, int part) { prod(0, 2 * i + 1, f, part); });
+    }
+  };
   uint32_t spins = 0;
   zero();
 #pragma unroll
@@ -351,13 +366,11 @@ __device__ __forceinline__ uint32_t gather_pair_mma(const Xchg& x, const int (&w
           const int i = i0 + ii;
           if (2 * i >= nf) continue;
           const bool v = 2 * i + hi < nf && bv;
-          Frag<MMA> f;
-          const bool fresh = xunpack<MMA>(r[ii], tag, f);
+          Op o;
+          const bool fresh = o.unpack(r[ii], tag);
           ok &= fresh || !v;
-          f = frag_keep<MMA>(v, f);
-          const Frag<MMA> odd = frag_rot8(f);
-          prod(0, 2 * i, frag_keep<MMA>(!hi, f));
-          if (2 * i + 1 < nf) prod(0, 2 * i + 1, frag_keep<MMA>(!hi, odd));
+          o.keep(v);
+          pair_prod(o, i);
         }
       } else {
 #pragma unroll
@@ -365,8 +378,8 @@ __device__ __forceinline__ uint32_t gather_pair_mma(const Xchg& x, const int (&w
           const int i = i0 + ii;
           if (i >= NP || 2 * i >= nf) continue;
           const bool v = 2 * i + hi < nf && bv;
-          Frag<MMA> f;
-          ok &= xunpack<MMA>(r[ii], tag, f) || !v;
+          Op o;
+          ok &= o.unpack(r[ii], tag) || !v;
         }
       }
       ++spins;
@@ -377,12 +390,10 @@ __device__ __forceinline__ uint32_t gather_pair_mma(const Xchg& x, const int (&w
             const int i = i0 + ii;
             if (i >= NP || 2 * i >= nf) continue;
             const bool v = 2 * i + hi < nf && bv;
-            Frag<MMA> f;
-            xunpack<MMA>(r[ii], tag, f);
-            f = frag_keep<MMA>(v, f);
-            const Frag<MMA> odd = frag_rot8(f);
-            prod(0, 2 * i, frag_keep<MMA>(!hi, f));
-            if (2 * i + 1 < nf) prod(0, 2 * i + 1, frag_keep<MMA>(!hi, odd));
+            Op o;
+            o.unpack(r[ii], tag);
+            o.keep(v);
+            pair_prod(o, i);
           }
         }
         break;
@@ -470,7 +481,8 @@ __device__ void fwd_io(const FwdArgs& a, const Team& tm, float* xring, float* os
     }
 #pragma unroll
     for (int v = 0; v < NV; ++v) {
-      if (v >= nst && !training) break;
+      if (v >= S && !training) break;
+      if (v < S && v >= nst) continue;  // the policy's states only: [nst,B,T,N,D]
       const f32x4 x = *reinterpret_cast<const f32x4*>(src + v * NE + e0);
       if (!el.real) continue;
       if (v < S)
@@ -484,8 +496,9 @@ __device__ void fwd_io(const FwdArgs& a, const Team& tm, float* xring, float* os
   // of step t+1, at the top of iteration t (steady state): P-2 iterations of
   // stores and loads.
   static_assert(P >= 2, "prefetch distance");
-  constexpr int kAfterTrain = (P - 2) * (GW + NV), kAfterFull = (P - 2) * (GW + S);
-  constexpr int kAfterHidden = (P - 2) * (GW + 1), kAfterLast = (P - 2) * GW;
+  // stores per step: the policy's states (S, 1 or none in the loop) plus the saves when training
+  constexpr int kAfterTrain = (P - 2) * (GW + NV), kAfterTrainHidden = (P - 2) * (GW + 1 + NSAVE);
+  constexpr int kAfterFull = (P - 2) * (GW + S), kAfterHidden = (P - 2) * (GW + 1), kAfterLast = (P - 2) * GW;
 
   Prof prof;
   prof.init(a.prof != nullptr && blockIdx.x == 0, a.prof != nullptr);
@@ -494,7 +507,8 @@ __device__ void fwd_io(const FwdArgs& a, const Team& tm, float* xring, float* os
   lds_barrier();  // Wx_0 in its slot
   for (int t = 0; t < T; ++t) {
     if (t + 1 >= P && t + P <= T) {
-      if (training) wait_vm<kAfterTrain>();
+      if (training && mode == 0) wait_vm<kAfterTrain>();
+      else if (training) wait_vm<kAfterTrainHidden>();
       else if (mode == 0) wait_vm<kAfterFull>();
       else if (mode == 1) wait_vm<kAfterHidden>();
       else wait_vm<kAfterLast>();
@@ -651,7 +665,7 @@ __global__ void __launch_bounds__(64 * (KSC + 1) * NDT) fwd_kernel(FwdArgs a) {
 #pragma unroll
         for (int g = 0; g < GR; ++g) acc[bt][g] = f32x4{0.f, 0.f, 0.f, 0.f};
     };
-    auto prod = [&](int bt, int j, const Frag<MMA>& f) {
+    auto prod = [&](int bt, int j, const Frag<MMA>& f, int) {
 #pragma unroll
       for (int g = 0; g < GR; ++g) acc[bt][g] = mma(A[g][j], f, acc[bt][g]);
     };
@@ -756,6 +770,7 @@ __device__ void bwd_io(const BwdArgs& a, const Team& tm, float* iring, float* os
   const Plan& p = a.p;
   const int T = p.T, N = p.N, D = p.D, B = p.B;
   const long wx_t = (long)GW * N * D;
+  const bool hidden_only = (p.flags & kFlagOutHidden) != 0;  // d_states [B,T,N,D]: the hidden state's only
   Elem el[IOQ];
   int e0[IOQ];
 #pragma unroll
@@ -769,8 +784,8 @@ __device__ void bwd_io(const BwdArgs& a, const Team& tm, float* iring, float* os
     for (int q = 0; q < IOQ; ++q) {
 #pragma unroll
       for (int k = 0; k < S; ++k)
-        dst[q][k] = (el[q].real && a.d_states)
-                        ? ld4_raw(a.d_states, ((((long)k * B + el[q].b) * T + t) * N + tm.n) * D + el[q].d, p.dt_io)
+        dst[q][k] = (el[q].real && a.d_states && (k == 0 || !hidden_only))
+                        ? ld4_raw(a.d_states, ((((long)k * B + el[q].b) * T + t) * N + tm.n) * D + el[q].d, p.dt_out)
                         : u32x4{0u, 0u, 0u, 0u};
 #pragma unroll
       for (int v = 0; v < NSAVE; ++v)
@@ -784,7 +799,7 @@ __device__ void bwd_io(const BwdArgs& a, const Team& tm, float* iring, float* os
     for (int q = 0; q < IOQ; ++q) {
       f32x4 v[NIN];
 #pragma unroll
-      for (int k = 0; k < S; ++k) v[k] = raw4_f32(src[q][k], p.dt_io);
+      for (int k = 0; k < S; ++k) v[k] = raw4_f32(src[q][k], p.dt_out);
 #pragma unroll
       for (int k = S; k < NIN; ++k) v[k] = __builtin_bit_cast(f32x4, src[q][k]);
       // transpose: element e0+m gets its NOP values contiguous
@@ -869,6 +884,11 @@ __global__ void __launch_bounds__(64 * (KSC + 1) * NDT) bwd_kernel(BwdArgs a) {
   const int D = p.D, B = p.B, N = p.N, T = p.T;
   const int GD = GR * D;
   const bool cut = (p.flags & kFlagCut) != 0;
+  const bool v1 = CELL == CELL_SLSTM && (p.flags & kFlagV1Grad) != 0;
+  // BF16 path: the gate cotangents travel as split words (hi + lo operands), so
+  // R^T dG is not computed from BF16-rounded dG (the reference's policy rounds the
+  // hidden state's cotangent after the product, not dG before it)
+  constexpr bool kSplit = MMA == MMA_BF16;
 
   constexpr int RED_B = Lds<CELL, NB>::RED_B;
   float* red = lds + tm.team * Lds<CELL, NB>::bwd(KS);  // [2][NB][KS][304]
@@ -981,7 +1001,7 @@ __global__ void __launch_bounds__(64 * (KSC + 1) * NDT) bwd_kernel(BwdArgs a) {
 #pragma unroll
       for (int v = 0; v < NSAVE; ++v) sv[v] = in[S + v];
       float dry[GR], dwx[GW], db[GT], cr[S];
-      Cell<CELL>::bwd(ds, sv, dry, dwx, db, cr);
+      Cell<CELL>::bwd(ds, sv, dry, dwx, db, cr, v1);
       if (!el[s].real) {
 #pragma unroll
         for (int g = 0; g < GR; ++g) dry[g] = 0.f;
@@ -1003,11 +1023,13 @@ __global__ void __launch_bounds__(64 * (KSC + 1) * NDT) bwd_kernel(BwdArgs a) {
       // the element's gate cotangents go out last (k = o * GR + g: one vector store when GR = 4)
       if (el[s].real && !cut) {
         if constexpr (MMA == MMA_BF16 && GR == 4) {  // k = 4d .. 4d+3: one aligned chunk
-          xstore_vec<MMA, GR>(xc, xoff + xgrp + xword_of<MMA>(p.BS, el[s].bl, el[s].d * GR), dry, step_tag(it));
+          xstore_vec<MMA, GR, kSplit>(xc, xoff + xgrp + xword_of<MMA>(p.BS, el[s].bl, el[s].d * GR), dry,
+                                      step_tag(it));
         } else {
 #pragma unroll
           for (int g = 0; g < GR; ++g)
-            xstore<MMA>(xc, xoff + xgrp + xword_of<MMA>(p.BS, el[s].bl, el[s].d * GR + g), dry[g], step_tag(it));
+            xstore<MMA, kSplit>(xc, xoff + xgrp + xword_of<MMA>(p.BS, el[s].bl, el[s].d * GR + g), dry[g],
+                                step_tag(it));
         }
       }
     }
@@ -1020,16 +1042,18 @@ __global__ void __launch_bounds__(64 * (KSC + 1) * NDT) bwd_kernel(BwdArgs a) {
 #pragma unroll
       for (int bt = 0; bt < NB; ++bt) acc[bt] = f32x4{0.f, 0.f, 0.f, 0.f};
     };
-    auto prod = [&](int bt, int j, const Frag<MMA>& f) { acc[bt] = mma(A[j], f, acc[bt]); };
+    // split words: the hi and lo products go into one accumulator (separate
+    // accumulators measured slower)
+    auto prod = [&](int bt, int j, const Frag<MMA>& f, int) { acc[bt] = mma(A[j], f, acc[bt]); };
     uint32_t polls = 0;
     if (cut)  // gradient_recurrent_cut: no R^T dG reaches h_{t-1}
       zero();
     else if (NB == 1 && pair)
-      polls = gather_pair_mma<MMA, NDT, NF>(xc, xword_pair, bv_pair, xoff, cstride, nkt, ptag(p, it), a.status,
-                                            a.spin_limit, abort, zero, prod);
+      polls = gather_pair_mma<MMA, NDT, NF, kSplit>(xc, xword_pair, bv_pair, xoff, cstride, nkt, ptag(p, it),
+                                                    a.status, a.spin_limit, abort, zero, prod);
     else
-      polls = gather_mma<MMA, NDT, NB, NF>(xc, xword, bval, xoff, cstride, nkt, ptag(p, it), a.status, a.spin_limit,
-                                           abort, zero, prod);
+      polls = gather_mma<MMA, NDT, NB, NF, kSplit>(xc, xword, bval, xoff, cstride, nkt, ptag(p, it), a.status,
+                                                   a.spin_limit, abort, zero, prod);
     prof.add(4, polls);
     prof.mark(0);
     prof.stamp(it, 2);

@@ -68,15 +68,24 @@ enum frnn_flags {
    * written, so each wait ends at the spin limit (frnn_set_spin_limit) with FRNN_E_TIMEOUT
    * and every wave leaves its loop. */
   FRNN_TEST_UNREADY = 16,
-  /* Forward-only output policies of FlashRNN2's prepared execution
-   * (flashrnn/flashrnn2/prepared.py:18-71, triton_persistent.py:154-166); not with
-   * FRNN_TRAINING. FRNN_OUT_HIDDEN: states_out is the hidden-state history only,
-   * [B,T,N,D]. FRNN_OUT_LAST: states_out is the hidden state of the sequence's last
-   * step only, [B,1,N,D], written by the call whose window ends the sequence.
-   * FRNN_SNAPSHOT_F32: states_out is FP32 instead of dtype_io. */
+  /* Output policies of FlashRNN2's prepared and training calls
+   * (flashrnn/flashrnn2/prepared.py:18-71, triton_persistent.py:154-166, training.py:91-124).
+   * FRNN_OUT_HIDDEN: states_out is the hidden-state history only, [B,T,N,D]; for
+   * frnn_bwd, states is that history and d_states is its cotangent, [B,T,N,D].
+   * FRNN_OUT_LAST (forward only, not with FRNN_TRAINING): states_out is the hidden
+   * state of the sequence's last step only, [B,1,N,D], written by the call whose
+   * window ends the sequence. FRNN_SNAPSHOT_F32: states_out (and, for frnn_bwd,
+   * states and d_states) are FP32 instead of dtype_io. A backward passes the flags of
+   * its training forward. */
   FRNN_OUT_HIDDEN = 32,
   FRNN_OUT_LAST = 64,
   FRNN_SNAPSHOT_F32 = 128,
+  /* sLSTM backward under the FlashRNN v1 gradient convention, which FlashRNN2's training
+   * keeps (flashrnn/flashrnn2/grad_reference.py:1-12, vanilla_fwbw/bw.py): the stabilizer
+   * m carries no cotangent (so the initial m's is zero) and the normalizer clamp
+   * max(n, 1) passes its cotangent straight through. Without it the backward is the
+   * exact gradient of flashrnn_torch (flashrnn2/reference.py:98-112). Other cells ignore it. */
+  FRNN_SLSTM_V1GRAD = 256,
 };
 
 typedef struct frnn_desc {

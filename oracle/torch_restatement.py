@@ -239,3 +239,62 @@ def flashrnn_torch_fused_options(
             gradient_recurrent_cut=gradient_recurrent_cut,
             gradient_recurrent_clipval=gradient_recurrent_clipval,
         )
+
+
+# ----------------------------------------------------------------------------
+# FlashRNN2's differentiable training call (``flashrnn/flashrnn2/training.py:91-124,
+# 214-228``): the forward of ``recurrence`` above, the requested output policy
+# taken from the state history (full [S,B,T,N,D], hidden [B,T,N,D] = history[0],
+# last [B,1,N,D] = history[0][:, -1:]) plus the final carry, and gradients under
+# the FlashRNN v1 convention of ``flashrnn/flashrnn2/grad_reference.py:1-60``:
+# for sLSTM the stabilizer m carries no gradient (neither the new m nor the
+# m_{t-1} inside log f) and the normalizer clamp max(., 1) is straight-through.
+# LSTM, GRU and Elman have no stabilizer or clamp: their gradients are exact.
+class _StraightMax1(torch.autograd.Function):
+    """max(x, 1) in the forward, identity in the backward (grad_reference.py:20-29)."""
+
+    @staticmethod
+    def forward(ctx, x):
+        return torch.maximum(x, torch.ones_like(x))
+
+    @staticmethod
+    def backward(ctx, g):
+        return g
+
+
+def _slstm_step_v1(x, ry, bias, state):
+    gi, gf, gz, go = (x + ry + bias).unbind(1)
+    _, c_old, n_old, m_old = state.unbind(0)
+    log_f = torch.nn.functional.logsigmoid(gf) + m_old.detach()
+    all_zero = torch.all(n_old == 0)
+    m = torch.where(all_zero, gi, torch.maximum(gi, log_f)).detach()
+    i_act = torch.exp(gi - m)
+    f_act = torch.exp(log_f - m)
+    c = f_act * c_old + i_act * torch.tanh(gz)
+    n = _StraightMax1.apply(f_act * n_old + i_act)
+    return torch.stack((torch.sigmoid(go) * c / n, c, n, m))
+
+
+def training_recurrence(
+    wx, recurrent, bias, initial, *, cell="lstm", numerics="mathematical", output_mode="hidden", v1_grad=True,
+):
+    """Returns (output, final [S,B,1,N,D]) of FlashRNN2's ``training.recurrence``;
+    ``v1_grad=False`` gives the exact gradient of flashrnn_torch instead."""
+    if output_mode not in ("full", "hidden", "last"):
+        raise ValueError("output mode must be full, hidden or last")
+    mma = torch.bfloat16 if numerics == "fp32_state_bf16_mma" else None
+    state = initial[:, :, 0]
+    history = []
+    with torch.autocast(wx.device.type, enabled=False):
+        for x in wx.unbind(1):
+            hidden = _round_through(state[0], mma)
+            weight = _round_through(recurrent, mma)
+            ry = torch.einsum("bnp,gnop->bgno", hidden, weight)
+            if cell == "slstm" and v1_grad:
+                state = _slstm_step_v1(x, ry, bias, state)
+            else:
+                state = _cell_step(cell, x, ry, bias, state)
+            history.append(state)
+    hist = torch.stack(history, dim=2)
+    out = hist if output_mode == "full" else (hist[0] if output_mode == "hidden" else hist[0][:, -1:])
+    return out, state.unsqueeze(2)

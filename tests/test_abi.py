@@ -110,7 +110,7 @@ def test_width_support(lib, cell, D, mma, ok):
         (_lib.FRNN_GRAD_CUT, 0.0, True), (_lib.FRNN_GRAD_CLIP, 0.25, True), (_lib.FRNN_GRAD_CLIP, 0.0, True),
         (_lib.FRNN_GRAD_CUT | _lib.FRNN_GRAD_CLIP, 1.0, True), (_lib.FRNN_GRAD_CLIP, -0.5, False),
         (_lib.FRNN_GRAD_CLIP, float("nan"), False), (_lib.FRNN_GRAD_CLIP, float("inf"), False),
-        (256, 0.0, False), (0, -3.0, True),  # without FRNN_GRAD_CLIP the value is ignored
+        (1024, 0.0, False), (0, -3.0, True),  # without FRNN_GRAD_CLIP the value is ignored
     ],
 )
 def test_option_flags(lib, flags, clipval, ok):
@@ -128,8 +128,10 @@ def test_option_flags(lib, flags, clipval, ok):
         (_lib.FRNN_SNAPSHOT_F32, 0, 0, True), (_lib.FRNN_OUT_HIDDEN | _lib.FRNN_SNAPSHOT_F32, 0, 0, True),
         (_lib.FRNN_OUT_HIDDEN | _lib.FRNN_OUT_LAST, 0, 0, False),  # one policy at a time
         (0, 12, 4, True), (0, 12, 8, True), (0, 12, 9, False), (0, 12, -1, False), (0, 3, 0, False),
-        (_lib.FRNN_TRAINING | _lib.FRNN_OUT_HIDDEN, 0, 0, False),  # forward-only policies
-        (_lib.FRNN_TRAINING | _lib.FRNN_SNAPSHOT_F32, 0, 0, False),
+        (_lib.FRNN_TRAINING | _lib.FRNN_OUT_HIDDEN, 0, 0, True),  # the backward needs the h history only
+        (_lib.FRNN_TRAINING | _lib.FRNN_SNAPSHOT_F32, 0, 0, True),
+        (_lib.FRNN_TRAINING | _lib.FRNN_OUT_LAST, 0, 0, False),  # forward-only policy
+        (_lib.FRNN_TRAINING | _lib.FRNN_SLSTM_V1GRAD, 0, 0, True),
         (_lib.FRNN_TRAINING, 12, 0, False),  # training needs the whole sequence
     ],
 )
@@ -138,8 +140,8 @@ def test_output_policy_and_window(lib, flags, total, base, ok):
     d = desc(T=4, flags=flags)
     d.total_steps, d.step_base = total, base
     assert (lib.frnn_workspace_bytes(ctypes.byref(d), 0) > 0) == ok
-    if ok and not flags & _lib.FRNN_TRAINING:
-        # the backward rejects every forward-only option before looking at its pointers
+    if ok:
+        # the backward rejects its invalid pointers, or a forward-only option before them
         assert lib.frnn_bwd(ctypes.byref(d), *([None] * 11), 0, None) == -1
 
 

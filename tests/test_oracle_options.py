@@ -143,3 +143,75 @@ def test_vanishing_clip_equals_cut(cell):
     # the initial state's cotangent is never clamped: only the cut removes its R^T dG part
     torch.testing.assert_close(a[5][1:], e[5][1:], atol=1e-25, rtol=1e-12)
     assert e[5][0].abs().max() == 0 and a[5][0].abs().max() > 0
+
+
+# ---------------------------------------------------------------- training call
+from oracle.torch_restatement import training_recurrence  # noqa: E402
+
+
+@pytest.mark.parametrize("cell", list(SIZES))
+@pytest.mark.parametrize("mode", ["full", "hidden", "last"])
+def test_training_forward_is_flashrnn_torch(cell, mode):
+    """Forward values (any gradient convention) and the output policy's selection."""
+    leaves = rand_inputs(cell)
+    out, fin = training_recurrence(*leaves, cell=cell, output_mode=mode)
+    hist, last = flashrnn_torch(*leaves, cell=cell)
+    exp = {"full": hist, "hidden": hist[0], "last": hist[0][:, -1:]}[mode]
+    torch.testing.assert_close(out, exp, atol=0, rtol=0)
+    torch.testing.assert_close(fin, last, atol=0, rtol=0)
+
+
+@pytest.mark.parametrize("cell", ["lstm", "gru", "elman"])
+def test_training_gradient_exact_without_stabilizer(cell):
+    """Cells without a stabilizer or clamp: the v1 convention is the exact gradient."""
+    leaves = rand_inputs(cell)
+    a, _ = run(lambda *l, cell: training_recurrence(*l, cell=cell, output_mode="full"), leaves, cell)
+    e, _ = run(flashrnn_torch, leaves, cell)
+    for x, y in zip(a[2:], e[2:]):
+        torch.testing.assert_close(x, y, atol=0, rtol=0)
+
+
+def _hidden_loss_grads(fn, leaves, seed=3):
+    out, fin = fn(*leaves)
+    g = torch.Generator().manual_seed(seed)
+    w = torch.randn(out.shape, generator=g, dtype=out.dtype)
+    wf = torch.randn(fin[0].shape, generator=g, dtype=fin.dtype)
+    return torch.autograd.grad((out * w).sum() + (fin[0] * wf).sum(), leaves)
+
+
+def test_slstm_v1_is_true_gradient_of_hidden_outputs():
+    """grad_reference.py:8-11: h does not depend on the stabilizer m, and with n0 >= 1
+    the clamp is never active (n' = f'n + i' > 1 since one of f', i' is 1); so for a
+    loss on the hidden states only the v1 convention gives the exact gradient of every
+    input except the initial m, whose v1 gradient is zero. The exact gradient of m0 is
+    not zero here (m0 enters m_1 through log f), which the convention drops."""
+    leaves = rand_inputs("slstm", T=6)  # n0 = |.| + 1 >= 1
+    with torch.no_grad():
+        assert (leaves[3][2] >= 1).all()
+    v1 = _hidden_loss_grads(lambda *l: training_recurrence(*l, cell="slstm", output_mode="hidden"), leaves)
+    ex = _hidden_loss_grads(lambda *l: training_recurrence(*l, cell="slstm", output_mode="hidden", v1_grad=False),
+                            leaves)
+    for x, y in zip(v1[:3], ex[:3]):
+        torch.testing.assert_close(x, y, atol=1e-12, rtol=1e-10)
+    torch.testing.assert_close(v1[3][:3], ex[3][:3], atol=1e-12, rtol=1e-10)
+    assert v1[3][3].abs().max() == 0
+
+
+def test_slstm_v1_at_the_clamp_tie():
+    """From a zero state the first step's normalizer is exactly 1, the clamp's tie:
+    torch.maximum gives each side half the cotangent, the straight-through clamp all
+    of it. h_1 = sig(o) tanh(z) does not depend on i or n_0 otherwise, so every
+    gradient agrees except the initial normalizer's, which v1 doubles; the initial m's
+    is zero in both (the predicate replaces m by i at the first step)."""
+    leaves = rand_inputs("slstm", T=3)
+    with torch.no_grad():
+        leaves[3].zero_()
+    v1 = _hidden_loss_grads(lambda *l: training_recurrence(*l, cell="slstm", output_mode="hidden"), leaves)
+    ex = _hidden_loss_grads(lambda *l: training_recurrence(*l, cell="slstm", output_mode="hidden", v1_grad=False),
+                            leaves)
+    for x, y in zip(v1[:3], ex[:3]):
+        torch.testing.assert_close(x, y, atol=1e-14, rtol=1e-12)
+    torch.testing.assert_close(v1[3][:2], ex[3][:2], atol=1e-14, rtol=1e-12)
+    assert ex[3][2].abs().max() > 0.1
+    torch.testing.assert_close(v1[3][2], 2 * ex[3][2], atol=1e-14, rtol=1e-12)
+    assert v1[3][3].abs().max() == 0 and ex[3][3].abs().max() == 0
