@@ -436,7 +436,7 @@ const char* frnn_strerror(int code) {
     case FRNN_E_WORKSPACE: return "workspace smaller than frnn_workspace_bytes()";
     case FRNN_E_LAUNCH: return "HIP kernel launch failed (co-residency or resources)";
     case FRNN_E_TIMEOUT: return "recurrence exchange timed out on the device";
-    case FRNN_E_PLACEMENT: return "a workgroup ran on an unexpected XCD; retry with FRNN_XCD_SHARED";
+    case FRNN_E_PLACEMENT: return "an XCD received more workgroups than its slots; retry with FRNN_XCD_SHARED";
   }
   return "unknown frnn error";
 }

@@ -340,6 +340,27 @@ struct Operand {
     if constexpr (SPLIT) return xunpack_split<MMA>(r, tag, hi, lo);
     else return xunpack<MMA>(r, tag, hi);
   }
+  // the tags alone (every word's tag equals `tag` iff the OR and the AND of the
+  // tag fields both do)
+  static __device__ __forceinline__ bool fresh(const Run<MMA>& r, uint32_t tag) {
+    if constexpr (MMA == MMA_BF16) {
+      uint32_t orv = 0u, andv = ~0u;
+#pragma unroll
+      for (int q = 0; q < 2; ++q)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          orv |= r.q[q][e];
+          andv &= r.q[q][e];
+        }
+      if constexpr (SPLIT) return ((orv & 3u) == tag) & ((andv & 3u) == tag);
+      else return ((orv >> 16) == tag) & ((andv >> 16) == tag);
+    } else {
+      bool ok = true;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) ok &= (r.q[q][1] == tag) & (r.q[q][3] == tag);
+      return ok;
+    }
+  }
   __device__ __forceinline__ void keep(bool k) {
     hi = frag_keep<MMA>(k, hi);
     if constexpr (SPLIT) lo = frag_keep<MMA>(k, lo);

@@ -206,6 +206,7 @@ struct Prof {
   }
 };
 
+
 // Runs a wave keeps in flight at most (8 BF16 runs or 4 FP32 runs: 64
 // registers; 4 runs in two-tile workgroups, whose resident slice is larger);
 // a longer contraction range is polled chunk by chunk, which bounds the
@@ -225,13 +226,13 @@ template <int MMA, int NDT> struct PollChunk {
 // Ranges of more than PollChunk runs are polled in chunks: each chunk is
 // polled until all of its tags are fresh and only then multiplied, so a
 // stale chunk never has to be taken back out of the accumulators.
-template <int MMA, int NDT, int NB, int NF, bool SPLIT = false, typename Zero, typename Prod>
+template <int MMA, int NDT, int NB, int NF, bool SPLIT = false, bool SPEC = true, typename Zero, typename Prod>
 __device__ __forceinline__ uint32_t gather_mma(const Xchg& x, const int (&word)[NB][NF], const bool (&bval)[NB],
                                                int off, int cstride, int nf, uint32_t tag, uint32_t* status, uint32_t spin_limit,
                                                bool& abort, Zero zero, Prod prod) {
   using Op = Operand<MMA, SPLIT>;
   uint32_t spins = 0;
-  if constexpr (NF <= PollChunk<MMA, NDT>::value) {
+  if constexpr (NF <= PollChunk<MMA, NDT>::value && SPEC) {
     while (true) {
       zero();
       if (abort) return spins;
@@ -267,7 +268,7 @@ __device__ __forceinline__ uint32_t gather_mma(const Xchg& x, const int (&word)[
       }
     }
   } else {
-    constexpr int CH = PollChunk<MMA, NDT>::value;
+    constexpr int CH = NF < PollChunk<MMA, NDT>::value ? NF : PollChunk<MMA, NDT>::value;
     zero();
 #pragma unroll
     for (int c0 = 0; c0 < NF; c0 += CH) {
@@ -287,10 +288,7 @@ __device__ __forceinline__ uint32_t gather_mma(const Xchg& x, const int (&word)[
         for (int bt = 0; bt < NB; ++bt)
 #pragma unroll
           for (int jj = 0; jj < CH; ++jj)
-            if (c0 + jj < NF && c0 + jj < nf) {
-              Op o;
-              ok &= o.unpack(r[bt][jj], tag) || !bval[bt];
-            }
+            if (c0 + jj < NF && c0 + jj < nf) ok &= Op::fresh(r[bt][jj], tag) || !bval[bt];
         ++spins;
         if (__all(ok)) {
 #pragma unroll
@@ -323,13 +321,16 @@ __device__ __forceinline__ uint32_t gather_mma(const Xchg& x, const int (&word)[
 // half the loads; the odd tile then moves down 8 lanes (DPP) and the upper
 // lanes contribute zero. word[j] is the run of k-tile j for batch row lane % 8.
 // Long ranges are polled in chunks of PollChunk pairs, as in gather_mma.
-template <int MMA, int NDT, int NF, bool SPLIT = false, typename Zero, typename Prod>
+template <int MMA, int NDT, int NF, bool SPLIT = false, bool SPEC = true, typename Zero, typename Prod>
 __device__ __forceinline__ uint32_t gather_pair_mma(const Xchg& x, const int (&word)[NF], bool bv, int off, int cstride, int nf,
                                                     uint32_t tag, uint32_t* status, uint32_t spin_limit, bool& abort,
                                                     Zero zero, Prod prod) {
   using Op = Operand<MMA, SPLIT>;
   constexpr int NP = (NF + 1) / 2;
   constexpr int CH = NP <= PollChunk<MMA, NDT>::value ? NP : PollChunk<MMA, NDT>::value;
+  // speculative: one chunk, multiplied while its tags are checked; otherwise
+  // each chunk is multiplied once all of its tags are fresh
+  constexpr bool kSpec = SPEC && NP <= PollChunk<MMA, NDT>::value;
   const int hi = (threadIdx.x >> 3) & 1;  // lane % 16 >= 8
   // the pair's products: the even tile in place, the odd one moved down 8 lanes
   auto pair_prod = [&](Op o, int i) {
@@ -348,7 +349,7 @@ __device__ __forceinline__ uint32_t gather_pair_mma(const Xchg& x, const int (&w
   for (int i0 = 0; i0 < NP; i0 += CH) {
     if (2 * i0 >= nf) break;
     while (true) {
-      if constexpr (NP <= PollChunk<MMA, NDT>::value) zero();
+      if constexpr (kSpec) zero();
       if (abort) return spins;
       Run<MMA> r[CH];
 #pragma unroll
@@ -359,8 +360,7 @@ __device__ __forceinline__ uint32_t gather_pair_mma(const Xchg& x, const int (&w
       }
       // Branch-free from here on (cross-lane DPP and MFMA need the whole wave).
       bool ok = true;
-      if constexpr (NP <= PollChunk<MMA, NDT>::value) {
-        // one chunk: multiply speculatively while the tags are checked
+      if constexpr (kSpec) {
 #pragma unroll
         for (int ii = 0; ii < CH; ++ii) {
           const int i = i0 + ii;
@@ -378,13 +378,12 @@ __device__ __forceinline__ uint32_t gather_pair_mma(const Xchg& x, const int (&w
           const int i = i0 + ii;
           if (i >= NP || 2 * i >= nf) continue;
           const bool v = 2 * i + hi < nf && bv;
-          Op o;
-          ok &= o.unpack(r[ii], tag) || !v;
+          ok &= Op::fresh(r[ii], tag) || !v;
         }
       }
       ++spins;
       if (__all(ok)) {
-        if constexpr (NP > PollChunk<MMA, NDT>::value) {
+        if constexpr (!kSpec) {
 #pragma unroll
           for (int ii = 0; ii < CH; ++ii) {
             const int i = i0 + ii;
@@ -887,8 +886,13 @@ __global__ void __launch_bounds__(64 * (KSC + 1) * NDT) bwd_kernel(BwdArgs a) {
   const bool v1 = CELL == CELL_SLSTM && (p.flags & kFlagV1Grad) != 0;
   // BF16 path: the gate cotangents travel as split words (hi + lo operands), so
   // R^T dG is not computed from BF16-rounded dG (the reference's policy rounds the
-  // hidden state's cotangent after the product, not dG before it)
+  // hidden state's cotangent after the product, not dG before it). Measured at
+  // C2: +0.17 ms of backward over BF16 words.
   constexpr bool kSplit = MMA == MMA_BF16;
+  // Polls check their tags before they unpack and multiply: a stale poll (the
+  // backward averages up to 2 per step) repeats at once instead of after a
+  // wasted product. Measured at C2: -0.17 ms against speculative products.
+  constexpr bool kSpecB = false;
 
   constexpr int RED_B = Lds<CELL, NB>::RED_B;
   float* red = lds + tm.team * Lds<CELL, NB>::bwd(KS);  // [2][NB][KS][304]
@@ -1042,18 +1046,18 @@ __global__ void __launch_bounds__(64 * (KSC + 1) * NDT) bwd_kernel(BwdArgs a) {
 #pragma unroll
       for (int bt = 0; bt < NB; ++bt) acc[bt] = f32x4{0.f, 0.f, 0.f, 0.f};
     };
-    // split words: the hi and lo products go into one accumulator (separate
-    // accumulators measured slower)
+    // split words: the hi and lo products go into one accumulator (a second
+    // accumulator for the lo products measured slower)
     auto prod = [&](int bt, int j, const Frag<MMA>& f, int) { acc[bt] = mma(A[j], f, acc[bt]); };
     uint32_t polls = 0;
     if (cut)  // gradient_recurrent_cut: no R^T dG reaches h_{t-1}
       zero();
     else if (NB == 1 && pair)
-      polls = gather_pair_mma<MMA, NDT, NF, kSplit>(xc, xword_pair, bv_pair, xoff, cstride, nkt, ptag(p, it),
-                                                    a.status, a.spin_limit, abort, zero, prod);
+      polls = gather_pair_mma<MMA, NDT, NF, kSplit, kSpecB>(xc, xword_pair, bv_pair, xoff, cstride, nkt,
+                                                            ptag(p, it), a.status, a.spin_limit, abort, zero, prod);
     else
-      polls = gather_mma<MMA, NDT, NB, NF, kSplit>(xc, xword, bval, xoff, cstride, nkt, ptag(p, it), a.status,
-                                                   a.spin_limit, abort, zero, prod);
+      polls = gather_mma<MMA, NDT, NB, NF, kSplit, kSpecB>(xc, xword, bval, xoff, cstride, nkt, ptag(p, it),
+                                                           a.status, a.spin_limit, abort, zero, prod);
     prof.add(4, polls);
     prof.mark(0);
     prof.stamp(it, 2);

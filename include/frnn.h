@@ -116,7 +116,7 @@ enum frnn_status {
   FRNN_E_WORKSPACE = -3,   /* workspace smaller than frnn_workspace_bytes() */
   FRNN_E_LAUNCH = -4,      /* the HIP runtime refused a launch (co-residency, resources) */
   FRNN_E_TIMEOUT = -5,     /* device: a recurrence exchange did not arrive within the spin limit */
-  FRNN_E_PLACEMENT = -6,   /* device: a workgroup ran on an unexpected XCD */
+  FRNN_E_PLACEMENT = -6,   /* device: an XCD received more workgroups than it has slots */
 };
 
 /* Gate and state counts of a cell: (G_R, G_W, G_T, S); flashrnn/flashrnn/flashrnn.py:45-70. */
@@ -128,16 +128,18 @@ int frnn_cell_sizes(int cell, int32_t* g_r, int32_t* g_w, int32_t* g_t, int32_t*
 size_t frnn_workspace_bytes(const frnn_desc* d, int which);
 
 /* Forward. Replaces FlashRNNFuncFused::forward (fused/flashrnn.cc:257-333).
- * states_out: [S,B,T,N,D] in dtype_io. carry_out: [S,B,N,D] in dtype_state
- * (may be NULL). save: the saved-for-backward area (may be NULL unless
- * FRNN_TRAINING). */
+ * states_out: [S,B,T,N,D] in dtype_io, or what the output-policy flags select
+ * (FRNN_OUT_HIDDEN, FRNN_OUT_LAST, FRNN_SNAPSHOT_F32; T = total_steps with a step
+ * window). carry_out: [S,B,N,D] in dtype_state (may be NULL). save: the
+ * saved-for-backward area (may be NULL unless FRNN_TRAINING). */
 int frnn_fwd(const frnn_desc* d, const void* wx, const void* R, const void* b, const void* s0,
              void* states_out, void* carry_out, void* save, void* ws, size_t ws_bytes,
              frnn_stream_t stream);
 
 /* Backward. Replaces FlashRNNFuncFused::backward (fused/flashrnn.cc:335-435).
  * R, s0, states (the forward's states_out) and save must be those of the
- * training forward. d_states: [S,B,T,N,D] (dtype_io, may be NULL = zero);
+ * training forward, and d carries its flags. d_states: [S,B,T,N,D] (dtype_io;
+ * [B,T,N,D] with FRNN_OUT_HIDDEN, FP32 with FRNN_SNAPSHOT_F32; may be NULL = zero);
  * d_carry: [S,B,N,D] (dtype_state, may be NULL = zero). Outputs dwx
  * [B,T,G_W,N,D], dR [G_R,N,D,D], db [G_T,N,D] (dtype_io) and ds0 [S,B,N,D]
  * (dtype_state) are overwritten. */
