@@ -14,8 +14,8 @@ import pathlib
 LIB_PATH = pathlib.Path(__file__).resolve().parent / "libfrnn.so"
 
 FRNN_LSTM, FRNN_GRU, FRNN_ELMAN, FRNN_SLSTM = 0, 1, 2, 3
-FRNN_F32, FRNN_BF16 = 0, 1
-FRNN_MMA_BF16, FRNN_MMA_F32 = 0, 1
+FRNN_F32, FRNN_BF16, FRNN_F16 = 0, 1, 2
+FRNN_MMA_BF16, FRNN_MMA_F32, FRNN_MMA_F16 = 0, 1, 2
 FRNN_TRAINING, FRNN_XCD_SHARED, FRNN_GRAD_CUT, FRNN_GRAD_CLIP, FRNN_TEST_UNREADY = 1, 2, 4, 8, 16
 FRNN_OUT_HIDDEN, FRNN_OUT_LAST, FRNN_SNAPSHOT_F32, FRNN_SLSTM_V1GRAD = 32, 64, 128, 256
 FRNN_OK = 0

@@ -107,10 +107,10 @@ bool fits(const Plan& p, int ks, bool forward) {
   const int waves = p.NDT * (ks + 1);
   const int per_simd = (waves + 3) / 4;
   const int budget = (512 / per_simd) / 8 * 8 - 56;
-  const int frag = p.mma == FRNN_MMA_BF16 ? 4 : 8;  // registers of one resident fragment
+  const int frag = p.mma == FRNN_MMA_F32 ? 8 : 4;  // registers of one resident fragment
   const int run = 2 * frag;                         // registers of one in-flight exchange run
   const int frags = p.GR * ktw;
-  const int runs = std::min(forward ? ktw : frags, (p.mma == FRNN_MMA_BF16 && p.NDT == 1) ? 8 : 4);
+  const int runs = std::min(forward ? ktw : frags, (p.mma != FRNN_MMA_F32 && p.NDT == 1) ? 8 : 4);
   return frags * frag + runs * run <= budget;
 }
 
@@ -126,9 +126,10 @@ int make_plan(const frnn_desc* d, Plan* p) {
   std::memset(p, 0, sizeof(*p));
   if (!cell_sizes(d->cell, &p->GR, &p->GW, &p->GT, &p->S)) return FRNN_E_INVALID;
   if (d->batch < 1 || d->steps < 1 || d->heads < 1 || d->width < 1) return FRNN_E_INVALID;
-  if (d->dtype_io != FRNN_F32 && d->dtype_io != FRNN_BF16) return FRNN_E_INVALID;
-  if (d->dtype_state != FRNN_F32 && d->dtype_state != FRNN_BF16) return FRNN_E_INVALID;
-  if (d->mma != FRNN_MMA_BF16 && d->mma != FRNN_MMA_F32) return FRNN_E_INVALID;
+  if (d->dtype_io != FRNN_F32 && d->dtype_io != FRNN_BF16 && d->dtype_io != FRNN_F16) return FRNN_E_INVALID;
+  if (d->dtype_state != FRNN_F32 && d->dtype_state != FRNN_BF16 && d->dtype_state != FRNN_F16)
+    return FRNN_E_INVALID;
+  if (d->mma != FRNN_MMA_BF16 && d->mma != FRNN_MMA_F32 && d->mma != FRNN_MMA_F16) return FRNN_E_INVALID;
   if (d->width % 32 != 0 || d->width > 1024) return FRNN_E_UNSUPPORTED;
   p->cell = d->cell;
   p->B = d->batch;
@@ -187,7 +188,7 @@ int make_plan(const frnn_desc* d, Plan* p) {
   p->wpg = p->D / (16 * p->NDT);
   set_groups(p, 0, p->ngroups);
   p->nwg = p->ngroups * p->wpg;
-  const long long wsz = p->mma == FRNN_MMA_BF16 ? 4 : 8;
+  const long long wsz = p->mma == FRNN_MMA_F32 ? 8 : 4;
   p->xwords_fwd = (long long)p->ngroups * p->BS * p->D;
   p->xwords_bwd = (long long)p->ngroups * p->BS * p->GR * p->D;
   p->save_floats = (long long)p->T * p->nwg * p->nsave * p->NDT * 256 * p->NB;
@@ -325,7 +326,7 @@ int frnn_fwd(const frnn_desc* d, const void* wx, const void* R, const void* b, c
   if (!fn) return FRNN_E_UNSUPPORTED;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   char* w = static_cast<char*>(ws);
-  const long long xbytes = 2 * p.xwords_fwd * (p.mma == FRNN_MMA_BF16 ? 4 : 8);
+  const long long xbytes = 2 * p.xwords_fwd * (p.mma == FRNN_MMA_F32 ? 8 : 4);
   if ((rc = clear(w + p.off_x, p.ws_fwd - p.off_x, st)) != FRNN_OK) return rc;  // exchange and claims
   frnn::FwdArgs a;
   a.p = p;
@@ -368,7 +369,7 @@ int frnn_bwd(const frnn_desc* d, const void* R, const void* s0, const void* stat
   if (!fn) return FRNN_E_UNSUPPORTED;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   char* w = static_cast<char*>(ws);
-  const long long xbytes = 2 * p.xwords_bwd * (p.mma == FRNN_MMA_BF16 ? 4 : 8);
+  const long long xbytes = 2 * p.xwords_bwd * (p.mma == FRNN_MMA_F32 ? 8 : 4);
   if ((rc = clear(w + p.off_x, p.off_dcand - p.off_x, st)) != FRNN_OK) return rc;  // exchange and claims
   frnn::BwdArgs a;
   a.p = p;

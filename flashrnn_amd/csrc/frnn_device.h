@@ -20,12 +20,15 @@ namespace frnn {
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned short u16x8 __attribute__((ext_vector_type(8)));
 
 enum { CELL_LSTM = 0, CELL_GRU = 1, CELL_ELMAN = 2, CELL_SLSTM = 3 };
-enum { MMA_BF16 = 0, MMA_F32 = 1 };
-enum { DT_F32 = 0, DT_BF16 = 1 };
+// Recurrent-product operand types; MMA_BF16 and MMA_F16 are the 16-bit family
+// (same exchange words and layouts, their own conversions and MFMA).
+enum { MMA_BF16 = 0, MMA_F32 = 1, MMA_F16 = 2 };
+enum { DT_F32 = 0, DT_BF16 = 1, DT_F16 = 2 };
 enum { ST_OK = 0, ST_TIMEOUT = 5, ST_PLACEMENT = 6 };
 
 // Cell shapes: recurrent gates, input gates, bias gates, states.
@@ -45,15 +48,28 @@ __device__ __forceinline__ uint32_t bf16_bits(float x) {
 }
 __device__ __forceinline__ float bf16_to_f32(uint32_t bits) { return u2f(bits << 16); }
 __device__ __forceinline__ float round_bf16(float x) { return bf16_to_f32(bf16_bits(x)); }
+// FP32 -> FP16 bits, round to nearest even (v_cvt_f16_f32), and back.
+__device__ __forceinline__ uint32_t f16_bits(float x) {
+  return (uint32_t)__builtin_bit_cast(unsigned short, (_Float16)x);
+}
+__device__ __forceinline__ float f16_to_f32(uint32_t bits) {
+  return (float)__builtin_bit_cast(_Float16, (unsigned short)bits);
+}
+__device__ __forceinline__ float round_f16(float x) { return f16_to_f32(f16_bits(x)); }
+// A 16-bit value of dtype dt (DT_BF16 or DT_F16) <-> FP32.
+__device__ __forceinline__ uint32_t h16_bits(float x, int dt) { return dt == DT_F16 ? f16_bits(x) : bf16_bits(x); }
+__device__ __forceinline__ float h16_to_f32(uint32_t bits, int dt) {
+  return dt == DT_F16 ? f16_to_f32(bits & 0xffffu) : bf16_to_f32(bits & 0xffffu);
+}
 
 // Loads/stores of the public tensors in their runtime dtype.
 __device__ __forceinline__ float ld_val(const void* p, long i, int dt) {
   if (dt == DT_F32) return static_cast<const float*>(p)[i];
-  return bf16_to_f32(static_cast<const unsigned short*>(p)[i]);
+  return h16_to_f32(static_cast<const unsigned short*>(p)[i], dt);
 }
 __device__ __forceinline__ void st_val(void* p, long i, int dt, float v) {
   if (dt == DT_F32) static_cast<float*>(p)[i] = v;
-  else static_cast<unsigned short*>(p)[i] = (unsigned short)bf16_bits(v);
+  else static_cast<unsigned short*>(p)[i] = (unsigned short)h16_bits(v, dt);
 }
 
 // Four consecutive values, raw: loads issue now and convert later (raw4_f32),
@@ -65,22 +81,25 @@ __device__ __forceinline__ u32x4 ld4_raw(const void* p, long i, int dt) {
 }
 __device__ __forceinline__ f32x4 raw4_f32(u32x4 r, int dt) {
   if (dt == DT_F32) return f32x4{u2f(r[0]), u2f(r[1]), u2f(r[2]), u2f(r[3])};
+  if (dt == DT_F16)
+    return f32x4{f16_to_f32(r[0] & 0xffffu), f16_to_f32(r[0] >> 16), f16_to_f32(r[1] & 0xffffu),
+                 f16_to_f32(r[1] >> 16)};
   return f32x4{u2f(r[0] << 16), u2f(r[0] & 0xffff0000u), u2f(r[1] << 16), u2f(r[1] & 0xffff0000u)};
 }
 
-// Four consecutive values (16-byte aligned in FP32, 8-byte aligned in BF16).
+// Four consecutive values (16-byte aligned in FP32, 8-byte aligned in 16 bits).
 __device__ __forceinline__ f32x4 ld4(const void* p, long i, int dt) {
   if (dt == DT_F32) return *reinterpret_cast<const f32x4*>(static_cast<const float*>(p) + i);
   const uint2 u = *reinterpret_cast<const uint2*>(static_cast<const unsigned short*>(p) + i);
-  return f32x4{u2f(u.x << 16), u2f(u.x & 0xffff0000u), u2f(u.y << 16), u2f(u.y & 0xffff0000u)};
+  return raw4_f32(u32x4{u.x, u.y, 0u, 0u}, dt);
 }
 __device__ __forceinline__ void st4(void* p, long i, int dt, f32x4 v) {
   if (dt == DT_F32) {
     *reinterpret_cast<f32x4*>(static_cast<float*>(p) + i) = v;
   } else {
     uint2 u;
-    u.x = bf16_bits(v[0]) | (bf16_bits(v[1]) << 16);
-    u.y = bf16_bits(v[2]) | (bf16_bits(v[3]) << 16);
+    u.x = h16_bits(v[0], dt) | (h16_bits(v[1], dt) << 16);
+    u.y = h16_bits(v[2], dt) | (h16_bits(v[3], dt) << 16);
     *reinterpret_cast<uint2*>(static_cast<unsigned short*>(p) + i) = u;
   }
 }
@@ -112,6 +131,10 @@ template <> struct Frag<MMA_BF16> {
   bf16x8 v;
   __device__ __forceinline__ void zero() { v = bf16x8{}; }
 };
+template <> struct Frag<MMA_F16> {
+  f16x8 v;
+  __device__ __forceinline__ void zero() { v = f16x8{}; }
+};
 template <> struct Frag<MMA_F32> {
   float v[8];
   __device__ __forceinline__ void zero() {
@@ -129,6 +152,11 @@ __device__ __forceinline__ f32x4 mma(const Frag<MMA_BF16>& a, const Frag<MMA_BF1
   asm("" : "+v"(bv));
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.v, bv, c, 0, 0, 0);
 }
+__device__ __forceinline__ f32x4 mma(const Frag<MMA_F16>& a, const Frag<MMA_F16>& b, f32x4 c) {
+  f16x8 bv = b.v;
+  asm("" : "+v"(bv));
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a.v, bv, c, 0, 0, 0);
+}
 __device__ __forceinline__ f32x4 mma(const Frag<MMA_F32>& a, const Frag<MMA_F32>& b, f32x4 c) {
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
@@ -143,7 +171,27 @@ __device__ __forceinline__ f32x4 mma(const Frag<MMA_F32>& a, const Frag<MMA_F32>
 __device__ __forceinline__ void frag_set(Frag<MMA_BF16>& f, int j, float x) {
   f.v[j] = __builtin_bit_cast(__bf16, (unsigned short)bf16_bits(x));
 }
+__device__ __forceinline__ void frag_set(Frag<MMA_F16>& f, int j, float x) { f.v[j] = (_Float16)x; }
 __device__ __forceinline__ void frag_set(Frag<MMA_F32>& f, int j, float x) { f.v[j] = x; }
+// Element j of a 16-bit fragment from its raw bits.
+__device__ __forceinline__ void frag_bits(Frag<MMA_BF16>& f, int j, uint32_t b) {
+  f.v[j] = __builtin_bit_cast(__bf16, (unsigned short)b);
+}
+__device__ __forceinline__ void frag_bits(Frag<MMA_F16>& f, int j, uint32_t b) {
+  f.v[j] = __builtin_bit_cast(_Float16, (unsigned short)b);
+}
+// Operand rounding of the 16-bit family, and its element bits.
+template <int MMA>
+__device__ __forceinline__ float round_op(float x) {
+  if constexpr (MMA == MMA_BF16) return round_bf16(x);
+  else if constexpr (MMA == MMA_F16) return round_f16(x);
+  else return x;
+}
+template <int MMA>
+__device__ __forceinline__ uint32_t op_bits(float x) {
+  if constexpr (MMA == MMA_F16) return f16_bits(x);
+  else return bf16_bits(x);
+}
 
 // Rotate a fragment by 8 lanes within each 16-lane row (DPP row_ror:8):
 // lane l receives lane l^8's value.
@@ -155,6 +203,15 @@ __device__ __forceinline__ Frag<MMA_BF16> frag_rot8(const Frag<MMA_BF16>& f) {
   for (int i = 0; i < 4; ++i) v[i] = rot8(v[i]);
   Frag<MMA_BF16> o;
   o.v = __builtin_bit_cast(bf16x8, v);
+  return o;
+}
+__device__ __forceinline__ Frag<MMA_F16> frag_rot8(const Frag<MMA_F16>& f) {
+  typedef int i32x4 __attribute__((ext_vector_type(4)));
+  i32x4 v = __builtin_bit_cast(i32x4, f.v);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) v[i] = rot8(v[i]);
+  Frag<MMA_F16> o;
+  o.v = __builtin_bit_cast(f16x8, v);
   return o;
 }
 __device__ __forceinline__ Frag<MMA_F32> frag_rot8(const Frag<MMA_F32>& f) {
@@ -171,7 +228,7 @@ __device__ __forceinline__ Frag<MMA> frag_keep(bool keep, const Frag<MMA>& f) {
 }
 
 // ------------------------------------------------------ exchange words
-// BF16 path: 32-bit word = (tag << 16) | bf16 bits.   F32 path: 64-bit word = (tag << 32) | f32 bits.
+// 16-bit paths: 32-bit word = (tag << 16) | bf16 or fp16 bits.   F32 path: 64-bit word = (tag << 32) | f32 bits.
 // Split words (the BF16 path's backward, whose exchanged gate cotangents are not
 // rounded to BF16 by the reference's policy): 32-bit word = the FP32 value rounded
 // to 21 mantissa bits, with the tag in the two lowest bits; the reader splits it
@@ -183,6 +240,7 @@ __device__ __forceinline__ uint32_t step_tag(int it) { return 1u + ((uint32_t)(i
 
 template <int MMA> struct Word;
 template <> struct Word<MMA_BF16> { typedef uint32_t type; };
+template <> struct Word<MMA_F16> { typedef uint32_t type; };
 template <> struct Word<MMA_F32> { typedef uint64_t type; };
 
 struct Xchg {
@@ -197,8 +255,8 @@ __device__ __forceinline__ uint32_t split_word(float v, uint32_t tag) { return (
 // in the shared L2); the placement-free mode uses an agent-scope store.
 template <int MMA, bool SPLIT = false>
 __device__ __forceinline__ void xstore(const Xchg& x, long word, float v, uint32_t tag) {
-  if constexpr (MMA == MMA_BF16) {
-    uint32_t w = SPLIT ? split_word(v, tag) : ((tag << 16) | bf16_bits(v));
+  if constexpr (MMA != MMA_F32) {
+    uint32_t w = SPLIT ? split_word(v, tag) : ((tag << 16) | op_bits<MMA>(v));
     uint32_t* p = reinterpret_cast<uint32_t*>(x.base) + word;
     if (x.shared_xcd) __hip_atomic_store(p, w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     else __builtin_nontemporal_store(w, p);
@@ -214,11 +272,11 @@ __device__ __forceinline__ void xstore(const Xchg& x, long word, float v, uint32
 // vector store.
 template <int MMA, int NV, bool SPLIT = false>
 __device__ __forceinline__ void xstore_vec(const Xchg& x, long word, const float* v, uint32_t tag) {
-  if constexpr (MMA == MMA_BF16 && NV == 4) {
+  if constexpr (MMA != MMA_F32 && NV == 4) {
     typedef uint32_t vec_t __attribute__((ext_vector_type(NV)));
     vec_t w;
 #pragma unroll
-    for (int i = 0; i < NV; ++i) w[i] = SPLIT ? split_word(v[i], tag) : ((tag << 16) | bf16_bits(v[i]));
+    for (int i = 0; i < NV; ++i) w[i] = SPLIT ? split_word(v[i], tag) : ((tag << 16) | op_bits<MMA>(v[i]));
     uint32_t* p = reinterpret_cast<uint32_t*>(x.base) + word;
     if (x.shared_xcd) {
 #pragma unroll
@@ -243,7 +301,7 @@ __device__ __forceinline__ void xstore_vec(const Xchg& x, long word, const float
 // whole 128-byte lines: the address unit handles one line per 8 lanes, not one
 // line per lane as with a [row][k] table (2.4x slower for the same bytes).
 template <int MMA> struct XLayout {
-  static constexpr int WP = MMA == MMA_BF16 ? 4 : 2;  // words per 16-byte chunk
+  static constexpr int WP = MMA == MMA_F32 ? 2 : 4;  // words per 16-byte chunk
   static constexpr int NC = 8 / WP;                   // chunks per run
 };
 template <int MMA>
@@ -256,8 +314,7 @@ __device__ __forceinline__ int xword_of(int BS, int r, int k) {
 // Issue the loads of one 8-word run (8 consecutive k) whose first chunk is at
 // word index `word`; its other chunks follow `cstride` bytes apart (16 * BS).
 // sc1 (aux 16) makes the load miss the CU-local L1 and read the L2.
-template <int MMA> struct Run;
-template <> struct Run<MMA_BF16> {
+template <int MMA> struct Run {  // 16-bit paths
   u32x4 q[2];
   __device__ __forceinline__ void zero() { q[0] = q[1] = u32x4{0u, 0u, 0u, 0u}; }
 };
@@ -269,7 +326,7 @@ template <> struct Run<MMA_F32> {
 template <int MMA>
 __device__ __forceinline__ void xload(const Xchg& x, int word, int cstride, Run<MMA>& r) {
   constexpr int NQ = XLayout<MMA>::NC;
-  const int byte = word * (MMA == MMA_BF16 ? 4 : 8);
+  const int byte = word * (MMA == MMA_F32 ? 8 : 4);
 #pragma unroll
   for (int q = 0; q < NQ; ++q) r.q[q] = __builtin_amdgcn_raw_buffer_load_b128(x.rsrc, byte + cstride * q, 0, 16);
 }
@@ -278,14 +335,14 @@ __device__ __forceinline__ void xload(const Xchg& x, int word, int cstride, Run<
 template <int MMA>
 __device__ __forceinline__ bool xunpack(const Run<MMA>& r, uint32_t tag, Frag<MMA>& f) {
   bool ok = true;
-  if constexpr (MMA == MMA_BF16) {
+  if constexpr (MMA != MMA_F32) {
 #pragma unroll
     for (int q = 0; q < 2; ++q)
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         uint32_t w = r.q[q][e];
         ok &= (w >> 16) == tag;
-        f.v[4 * q + e] = __builtin_bit_cast(__bf16, (unsigned short)(w & 0xffffu));
+        frag_bits(f, 4 * q + e, w & 0xffffu);
       }
   } else {
 #pragma unroll
@@ -306,29 +363,56 @@ __device__ __forceinline__ bool xunpack(const Run<MMA>& r, uint32_t tag, Frag<MM
 // Per pair of words: one byte permute (hi), two masks and subtractions and one
 // packed conversion (lo); the tags of the 8 words are checked together: every
 // word's low two bits equal tag iff both their OR and their AND do.
+//
+// FP16: hi = the value converted with round-toward-zero (one packed conversion
+// per pair), lo = the exact remainder converted the same way: about 22
+// significant bits, within FP16's exponent range.
 template <int MMA>
 __device__ __forceinline__ bool xunpack_split(const Run<MMA>& r, uint32_t tag, Frag<MMA>& hi, Frag<MMA>& lo) {
-  static_assert(MMA == MMA_BF16, "split words exist on the BF16 path only");
-  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
-  typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
-  u32x4_t hp, lp;
-  uint32_t orv = 0u, andv = ~0u;
+  static_assert(MMA != MMA_F32, "split words exist on the 16-bit paths only");
+  if constexpr (MMA == MMA_F16) {
+    typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+    typedef __fp16 fp16x2_t __attribute__((ext_vector_type(2)));
+    uint32_t orv = 0u, andv = ~0u;
 #pragma unroll
-  for (int q = 0; q < 2; ++q)
+    for (int q = 0; q < 2; ++q)
 #pragma unroll
-    for (int e = 0; e < 4; e += 2) {
-      const uint32_t w0 = r.q[q][e], w1 = r.q[q][e + 1];
-      hp[2 * q + e / 2] = __builtin_amdgcn_perm(w1, w0, 0x07060302u);
-      const float l0 = u2f(w0) - u2f(w0 & 0xffff0000u);
-      const float l1 = u2f(w1) - u2f(w1 & 0xffff0000u);
-      const bf16x2_t l = {(__bf16)l0, (__bf16)l1};
-      lp[2 * q + e / 2] = __builtin_bit_cast(uint32_t, l);
-      orv |= w0 | w1;
-      andv &= w0 & w1;
-    }
-  hi.v = __builtin_bit_cast(bf16x8, hp);
-  lo.v = __builtin_bit_cast(bf16x8, lp);
-  return ((orv & 3u) == tag) & ((andv & 3u) == tag);
+      for (int e = 0; e < 4; e += 2) {
+        const uint32_t w0 = r.q[q][e], w1 = r.q[q][e + 1];
+        const float v0 = u2f(w0 & ~3u), v1 = u2f(w1 & ~3u);
+        const f16x2_t h = __builtin_bit_cast(f16x2_t, (fp16x2_t)__builtin_amdgcn_cvt_pkrtz(v0, v1));
+        const f16x2_t l =
+            __builtin_bit_cast(f16x2_t, (fp16x2_t)__builtin_amdgcn_cvt_pkrtz(v0 - (float)h[0], v1 - (float)h[1]));
+        hi.v[4 * q + e] = h[0];
+        hi.v[4 * q + e + 1] = h[1];
+        lo.v[4 * q + e] = l[0];
+        lo.v[4 * q + e + 1] = l[1];
+        orv |= w0 | w1;
+        andv &= w0 & w1;
+      }
+    return ((orv & 3u) == tag) & ((andv & 3u) == tag);
+  } else {
+    typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+    typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+    u32x4_t hp, lp;
+    uint32_t orv = 0u, andv = ~0u;
+  #pragma unroll
+    for (int q = 0; q < 2; ++q)
+  #pragma unroll
+      for (int e = 0; e < 4; e += 2) {
+        const uint32_t w0 = r.q[q][e], w1 = r.q[q][e + 1];
+        hp[2 * q + e / 2] = __builtin_amdgcn_perm(w1, w0, 0x07060302u);
+        const float l0 = u2f(w0) - u2f(w0 & 0xffff0000u);
+        const float l1 = u2f(w1) - u2f(w1 & 0xffff0000u);
+        const bf16x2_t l = {(__bf16)l0, (__bf16)l1};
+        lp[2 * q + e / 2] = __builtin_bit_cast(uint32_t, l);
+        orv |= w0 | w1;
+        andv &= w0 & w1;
+      }
+    hi.v = __builtin_bit_cast(bf16x8, hp);
+    lo.v = __builtin_bit_cast(bf16x8, lp);
+    return ((orv & 3u) == tag) & ((andv & 3u) == tag);
+  }
 }
 
 // Unpack a run into the operand(s) of its product: one fragment, or with split
@@ -343,7 +427,7 @@ struct Operand {
   // the tags alone (every word's tag equals `tag` iff the OR and the AND of the
   // tag fields both do)
   static __device__ __forceinline__ bool fresh(const Run<MMA>& r, uint32_t tag) {
-    if constexpr (MMA == MMA_BF16) {
+    if constexpr (MMA != MMA_F32) {
       uint32_t orv = 0u, andv = ~0u;
 #pragma unroll
       for (int q = 0; q < 2; ++q)

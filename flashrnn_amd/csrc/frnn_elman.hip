@@ -30,7 +30,12 @@ static const void* by_shape(int ks, int ktw, int ndt, bool fwd) {
 }
 
 const void* elman_kernel(int mma, int ks, int ktw, int ndt, bool forward) {
-  return mma == MMA_BF16 ? by_shape<MMA_BF16>(ks, ktw, ndt, forward) : by_shape<MMA_F32>(ks, ktw, ndt, forward);
+  switch (mma) {
+    case MMA_BF16: return by_shape<MMA_BF16>(ks, ktw, ndt, forward);
+    case MMA_F16: return by_shape<MMA_F16>(ks, ktw, ndt, forward);
+    case MMA_F32: return by_shape<MMA_F32>(ks, ktw, ndt, forward);
+  }
+  return nullptr;
 }
 
 long elman_lds_floats(bool forward, int ks) {

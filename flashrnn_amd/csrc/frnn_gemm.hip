@@ -26,7 +26,7 @@ template <> struct GemmElem<MMA_F32> { typedef float type; };
 
 template <int MMA>
 __device__ __forceinline__ typename GemmElem<MMA>::type gemm_cvt(float v) {
-  if constexpr (MMA == MMA_BF16) return (unsigned short)bf16_bits(v);
+  if constexpr (MMA != MMA_F32) return (unsigned short)op_bits<MMA>(v);
   else return v;
 }
 
@@ -34,6 +34,8 @@ template <int MMA>
 __device__ __forceinline__ void gemm_frag(const typename GemmElem<MMA>::type* row, Frag<MMA>& f) {
   if constexpr (MMA == MMA_BF16) {
     f.v = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u16x8*>(row));
+  } else if constexpr (MMA == MMA_F16) {
+    f.v = __builtin_bit_cast(f16x8, *reinterpret_cast<const u16x8*>(row));
   } else {
     const f32x4 lo = *reinterpret_cast<const f32x4*>(row);
     const f32x4 hi = *reinterpret_cast<const f32x4*>(row + 4);
@@ -203,12 +205,18 @@ __global__ void __launch_bounds__(256) clear_kernel(uint32_t* p, long n) {
   for (long i = blockIdx.x * 256L + threadIdx.x; i < n; i += (long)gridDim.x * 256) p[i] = 0u;
 }
 
+template <int MMA>
+static const void* gemm_of(bool wide) {
+  return wide ? reinterpret_cast<const void*>(&dr_gemm_kernel<MMA, 2, 2>)
+              : reinterpret_cast<const void*>(&dr_gemm_kernel<MMA, 1, 1>);
+}
 const void* gemm_kernel(int mma, bool wide) {
-  if (wide)
-    return mma == MMA_BF16 ? reinterpret_cast<const void*>(&dr_gemm_kernel<MMA_BF16, 2, 2>)
-                           : reinterpret_cast<const void*>(&dr_gemm_kernel<MMA_F32, 2, 2>);
-  return mma == MMA_BF16 ? reinterpret_cast<const void*>(&dr_gemm_kernel<MMA_BF16, 1, 1>)
-                         : reinterpret_cast<const void*>(&dr_gemm_kernel<MMA_F32, 1, 1>);
+  switch (mma) {
+    case MMA_BF16: return gemm_of<MMA_BF16>(wide);
+    case MMA_F16: return gemm_of<MMA_F16>(wide);
+    case MMA_F32: return gemm_of<MMA_F32>(wide);
+  }
+  return nullptr;
 }
 const void* reduce_kernel() { return reinterpret_cast<const void*>(&dr_reduce_kernel); }
 const void* zero_kernel() { return reinterpret_cast<const void*>(&clear_kernel); }

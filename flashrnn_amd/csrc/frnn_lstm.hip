@@ -24,7 +24,7 @@ static const void* by_shape(int ks, int ktw, int ndt, bool fwd) {
   if (ndt == 1 && ks == 4 && ktw == 4) return pick<MMA, 4, 1, 4>(fwd);
   if (ndt == 1 && ks == 8 && ktw == 1) return pick<MMA, 1, 1, 8>(fwd);
   if (ndt == 1 && ks == 8 && ktw == 2) return pick<MMA, 2, 1, 8>(fwd);
-  if constexpr (MMA == MMA_BF16) {  // two-tile workgroups: only the BF16 slice fits beside the runs
+  if constexpr (MMA != MMA_F32) {  // two-tile workgroups: only a 16-bit slice fits beside the runs
     if (ndt == 2 && ks == 3 && ktw == 6) return pick<MMA, 6, 2, 3>(fwd);
     if (ndt == 2 && ks == 3 && ktw == 8) return pick<MMA, 8, 2, 3>(fwd);
   }
@@ -32,7 +32,12 @@ static const void* by_shape(int ks, int ktw, int ndt, bool fwd) {
 }
 
 const void* lstm_kernel(int mma, int ks, int ktw, int ndt, bool forward) {
-  return mma == MMA_BF16 ? by_shape<MMA_BF16>(ks, ktw, ndt, forward) : by_shape<MMA_F32>(ks, ktw, ndt, forward);
+  switch (mma) {
+    case MMA_BF16: return by_shape<MMA_BF16>(ks, ktw, ndt, forward);
+    case MMA_F16: return by_shape<MMA_F16>(ks, ktw, ndt, forward);
+    case MMA_F32: return by_shape<MMA_F32>(ks, ktw, ndt, forward);
+  }
+  return nullptr;
 }
 
 long lstm_lds_floats(bool forward, int ks) {

@@ -212,7 +212,7 @@ struct Prof {
 // a longer contraction range is polled chunk by chunk, which bounds the
 // registers of the in-flight loads.
 template <int MMA, int NDT> struct PollChunk {
-  static constexpr int value = (MMA == MMA_BF16 && NDT == 1) ? 8 : 4;
+  static constexpr int value = (MMA != MMA_F32 && NDT == 1) ? 8 : 4;
 };
 
 // Poll the exchange and run the step's product on it, fused. Every 8-word run
@@ -428,7 +428,7 @@ __device__ __forceinline__ void wait_vm() {
 __device__ __forceinline__ float ring_x(const float* slot, int g, int r, int d, int dt) {
   if (dt == DT_F32) return slot[(g * 64 + r * 4 + (d >> 2)) * 4 + (d & 3)];
   const unsigned short* h = reinterpret_cast<const unsigned short*>(slot);
-  return bf16_to_f32(h[(g * 64 + r * 4 + (d >> 3) * 2) * 8 + (d & 7)]);
+  return h16_to_f32(h[(g * 64 + r * 4 + (d >> 3) * 2) * 8 + (d & 7)], dt);
 }
 
 // I/O wave of a team. Wx of step u is loaded straight into ring slot
@@ -884,11 +884,11 @@ __global__ void __launch_bounds__(64 * (KSC + 1) * NDT) bwd_kernel(BwdArgs a) {
   const int GD = GR * D;
   const bool cut = (p.flags & kFlagCut) != 0;
   const bool v1 = CELL == CELL_SLSTM && (p.flags & kFlagV1Grad) != 0;
-  // BF16 path: the gate cotangents travel as split words (hi + lo operands), so
-  // R^T dG is not computed from BF16-rounded dG (the reference's policy rounds the
+  // 16-bit paths: the gate cotangents travel as split words (hi + lo operands),
+  // so R^T dG is not computed from rounded dG (the reference's policy rounds the
   // hidden state's cotangent after the product, not dG before it). Measured at
   // C2: +0.17 ms of backward over BF16 words.
-  constexpr bool kSplit = MMA == MMA_BF16;
+  constexpr bool kSplit = MMA != MMA_F32;
   // Polls check their tags before they unpack and multiply: a stale poll (the
   // backward averages up to 2 per step) repeats at once instead of after a
   // wasted product. Measured at C2: -0.17 ms against speculative products.
@@ -1026,7 +1026,7 @@ __global__ void __launch_bounds__(64 * (KSC + 1) * NDT) bwd_kernel(BwdArgs a) {
       *reinterpret_cast<f32x4*>(os + e * NOB) = ov;
       // the element's gate cotangents go out last (k = o * GR + g: one vector store when GR = 4)
       if (el[s].real && !cut) {
-        if constexpr (MMA == MMA_BF16 && GR == 4) {  // k = 4d .. 4d+3: one aligned chunk
+        if constexpr (MMA != MMA_F32 && GR == 4) {  // k = 4d .. 4d+3: one aligned chunk
           xstore_vec<MMA, GR, kSplit>(xc, xoff + xgrp + xword_of<MMA>(p.BS, el[s].bl, el[s].d * GR), dry,
                                       step_tag(it));
         } else {
@@ -1082,7 +1082,7 @@ __global__ void __launch_bounds__(64 * (KSC + 1) * NDT) bwd_kernel(BwdArgs a) {
 #pragma unroll
       for (int w2 = 0; w2 < KS; ++w2) v += part[w2];
       // the BF16 policy rounds the cotangent of the rounded hidden operand
-      dhrec[s] = el[s].real ? (MMA == MMA_BF16 ? round_bf16(v) : v) : 0.f;
+      dhrec[s] = el[s].real ? round_op<MMA>(v) : 0.f;
     }
     prof.mark(6);
     prof.stamp(it, 4);

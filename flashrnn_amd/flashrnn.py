@@ -15,7 +15,9 @@ Numerics. ``dtype="bfloat16"`` (the default, as in the reference) runs the
 recurrent product with BF16 operands and FP32 accumulation and keeps every
 state and the pointwise cell in FP32: the reference's
 ``numerics="fp32_state_bf16_mma"`` policy (``flashrnn2/torch_backend.py:21-35``).
-``dtype="float32"`` runs the product in FP32 (the mathematical policy).
+``dtype="float16"`` does the same with FP16 operands (FlashRNN2's FP16
+contract: FP16 inputs, FP32 compute and state). ``dtype="float32"`` runs the
+product in FP32 (the mathematical policy).
 Inputs may be BF16 or FP32 in either mode; outputs use the dtype of ``Wx``.
 
 ``last`` is the full-precision carry: it has the dtype of the ``states``
@@ -38,8 +40,11 @@ from . import _lib
 # (G_R, G_W, G_T, S); rnn_function_registry, flashrnn/flashrnn/flashrnn.py:45-70
 CELL_SIZES = {"lstm": (4, 4, 4, 2), "slstm": (4, 4, 4, 4), "gru": (3, 3, 4, 1), "elman": (1, 1, 1, 1)}
 FUSED_BACKENDS = ("cuda_fused", "fused", "hip_fused")
-DTYPES = {"bfloat16": torch.bfloat16, "float32": torch.float32}
-_IO = {torch.float32: _lib.FRNN_F32, torch.bfloat16: _lib.FRNN_BF16}
+DTYPES = {"bfloat16": torch.bfloat16, "float16": torch.float16, "float32": torch.float32}
+_IO = {torch.float32: _lib.FRNN_F32, torch.bfloat16: _lib.FRNN_BF16, torch.float16: _lib.FRNN_F16}
+# recurrent-product operand type of a config dtype (or of an input dtype)
+_MMA = {"bfloat16": _lib.FRNN_MMA_BF16, "float16": _lib.FRNN_MMA_F16, "float32": _lib.FRNN_MMA_F32}
+_MMA_OF = {torch.bfloat16: _lib.FRNN_MMA_BF16, torch.float16: _lib.FRNN_MMA_F16, torch.float32: _lib.FRNN_MMA_F32}
 
 
 @dataclass
@@ -244,8 +249,8 @@ def flashrnn(
     _check_shapes(cell, Wx, R, b, states)
     io = Wx.dtype if Wx.dtype in _IO else torch.float32
     if Wx.dtype not in _IO:
-        raise ValueError(f"Wx dtype {Wx.dtype} not supported; use bfloat16 or float32")
-    mma = _lib.FRNN_MMA_BF16 if config.dtype == "bfloat16" else _lib.FRNN_MMA_F32
+        raise ValueError(f"Wx dtype {Wx.dtype} not supported; use bfloat16, float16 or float32")
+    mma = _MMA[config.dtype]
     B, T, _, N, D = Wx.shape
     S = CELL_SIZES[cell][3]
     if states is None:

@@ -22,8 +22,8 @@ buffers alternate), so a chunked run equals the unchunked run bitwise.
 
 Differences from the reference, on purpose: every cell of the fused path is
 accepted (the reference's prepared path has LSTM and sLSTM only), Wx has the
-cell's own gate count, inputs are BF16 (recurrent product with BF16 operands,
-FP32 accumulation and state -- the same arithmetic as the reference's BF16
+cell's own gate count, inputs are BF16 or FP16 (recurrent product with 16-bit
+operands, FP32 accumulation and state -- the arithmetic of the reference's
 prepared kernels) or FP32 (FP32 product); the head width must be a multiple
 of 32 (at most 1024) because padding would break the fixed input addresses;
 ``config`` is this library's :class:`KernelConfig`, not the reference's
@@ -38,7 +38,7 @@ from dataclasses import dataclass
 import torch
 
 from . import _lib
-from .flashrnn import CELL_SIZES, _IO, _state
+from .flashrnn import _IO, _MMA_OF, CELL_SIZES, _state
 
 _MODES = {"full": 0, "hidden": _lib.FRNN_OUT_HIDDEN, "last": _lib.FRNN_OUT_LAST}
 
@@ -94,7 +94,7 @@ class PreparedSequence:
             raise ValueError("invalid initial-state shape")
         tensors = (wx, recurrent, bias, initial)
         if wx.dtype not in _IO:
-            raise ValueError("inputs must be bfloat16 or float32")
+            raise ValueError("inputs must be bfloat16, float16 or float32")
         if recurrent.dtype != wx.dtype or bias.dtype != wx.dtype or initial.dtype not in (wx.dtype, torch.float32):
             raise ValueError("input dtype does not match generic computation contract")
         if any(x.requires_grad for x in tensors):
@@ -129,7 +129,7 @@ class PreparedSequence:
         flags = _MODES[output_mode] | (_lib.FRNN_SNAPSHOT_F32 if dtype == torch.float32 else 0)
         flags |= _lib.FRNN_XCD_SHARED if exchange == "shared" else 0
         flags |= _lib.FRNN_TEST_UNREADY if _state["test_unready"] else 0  # failure-handling tests only
-        mma = _lib.FRNN_MMA_BF16 if wx.dtype == torch.bfloat16 else _lib.FRNN_MMA_F32
+        mma = _MMA_OF[wx.dtype]
         lib = _lib.load()
         self._descs, start = [], 0
         for n in lengths:

@@ -22,8 +22,8 @@ GEMM reads nothing else), in FP32 when ``snapshot_dtype`` is FP32. ``last``
 returns the final step of that history, and its cotangent joins the carry's.
 
 Differences from the reference, on purpose: every cell of the fused path is
-accepted (the reference trains LSTM and sLSTM only); inputs are BF16 (BF16
-recurrent-product operands, FP32 accumulation and state) or FP32 (FP32
+accepted (the reference trains LSTM and sLSTM only); inputs are BF16 or FP16
+(16-bit recurrent-product operands, FP32 accumulation and state) or FP32 (FP32
 product); ``config`` is :class:`flashrnn_amd.prepared.KernelConfig`;
 ``backward_options`` (the reference's Triton/CUDA backward tuning knobs) must be
 empty: this backward has one kernel. A ``sequence_context`` past the first step
@@ -36,7 +36,7 @@ import torch
 import torch.nn.functional as F
 
 from . import _lib
-from .flashrnn import CELL_SIZES, _IO, _after_call, _drain_pending, _state, _workspace
+from .flashrnn import _IO, _MMA_OF, CELL_SIZES, _after_call, _drain_pending, _state, _workspace
 from .prepared import KernelConfig, default_config
 
 
@@ -62,7 +62,7 @@ class _Recurrence(torch.autograd.Function):
         snap = wx.dtype if snapshot_dtype is None else snapshot_dtype
         training = torch.is_grad_enabled() or any(ctx.needs_input_grad[:4])
         flags = _flags(output_mode, snap == torch.float32 and snap != wx.dtype, cell, config, training)
-        mma = _lib.FRNN_MMA_BF16 if wx.dtype == torch.bfloat16 else _lib.FRNN_MMA_F32
+        mma = _MMA_OF[wx.dtype]
         d = _lib.FrnnDesc(_lib.CELLS[cell], B, T, N, D, _IO[wx.dtype], _lib.FRNN_F32, mma, flags, 0.0, 0, 0)
         s0 = initial[:, :, 0].to(torch.float32).contiguous()  # exact; the carry is FP32
         hist = torch.empty((S, B, T, N, D) if output_mode == "full" else (B, T, N, D), dtype=snap, device=dev)
@@ -139,7 +139,7 @@ def recurrence(wx, recurrent, bias, initial, cell="lstm", *, output_mode="hidden
     if initial.shape != (S, B, 1, N, D):
         raise ValueError("invalid initial-state shape")
     if wx.dtype not in _IO:
-        raise ValueError("inputs must be bfloat16 or float32")
+        raise ValueError("inputs must be bfloat16, float16 or float32")
     if recurrent.dtype != wx.dtype or bias.dtype != wx.dtype or initial.dtype not in (wx.dtype, torch.float32):
         raise ValueError("input dtype does not match generic computation contract")
     if not wx.is_cuda or any(t.device != wx.device for t in (recurrent, bias, initial)):

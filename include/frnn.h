@@ -42,14 +42,16 @@ extern "C" {
 typedef struct ihipStream_t* frnn_stream_t; /* == hipStream_t */
 
 enum frnn_cell { FRNN_LSTM = 0, FRNN_GRU = 1, FRNN_ELMAN = 2, FRNN_SLSTM = 3 };
-enum frnn_dtype { FRNN_F32 = 0, FRNN_BF16 = 1 };
+enum frnn_dtype { FRNN_F32 = 0, FRNN_BF16 = 1, FRNN_F16 = 2 };
 /* Recurrent-product arithmetic:
  *  FRNN_MMA_BF16: R and h_{t-1} rounded to BF16, FP32 accumulation, FP32
  *    state and pointwise -- the reference's numerics="fp32_state_bf16_mma"
  *    (flashrnn/flashrnn2/torch_backend.py:21-35). Backward rounds the
  *    recurrent cotangents through BF16 the same way.
- *  FRNN_MMA_F32: FP32 operands and accumulation -- numerics="mathematical" in FP32. */
-enum frnn_mma { FRNN_MMA_BF16 = 0, FRNN_MMA_F32 = 1 };
+ *  FRNN_MMA_F32: FP32 operands and accumulation -- numerics="mathematical" in FP32.
+ *  FRNN_MMA_F16: as FRNN_MMA_BF16 with FP16 operands: FlashRNN2's FP16 contract (FP16
+ *    inputs, FP32 compute and state; flashrnn/flashrnn2/state_contract.py:21-49). */
+enum frnn_mma { FRNN_MMA_BF16 = 0, FRNN_MMA_F32 = 1, FRNN_MMA_F16 = 2 };
 enum frnn_flags {
   FRNN_TRAINING = 1,       /* frnn_fwd fills the saved-for-backward area */
   FRNN_XCD_SHARED = 2,     /* exchange through memory-side coherence (slower; any placement) */

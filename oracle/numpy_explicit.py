@@ -16,7 +16,10 @@ The backward here is the one the HIP kernels implement:
 * torch tie rules: ``maximum(a, b)`` sends half the cotangent to each input
   on a tie; ``where`` sends all of it to the selected input.
 
-BF16 rounding is round-to-nearest-even by bit manipulation on FP32.
+BF16 rounding is round-to-nearest-even by bit manipulation on FP32. FP16
+rounding (``operands="f16"``: the same policy with FP16 operands, FlashRNN2's
+FP16 contract of ``flashrnn/flashrnn2/state_contract.py:21-49``) is NumPy's own
+float16 conversion, independent of torch's.
 """
 
 from __future__ import annotations
@@ -35,6 +38,17 @@ def bf16_round(x: np.ndarray) -> np.ndarray:
     return np.where(np.isnan(x32), x32, out)
 
 
+def f16_round(x: np.ndarray) -> np.ndarray:
+    """FP32 -> FP16 (NumPy's round to nearest even) -> FP32."""
+    return np.asarray(x, dtype=np.float32).astype(np.float16).astype(np.float32)
+
+
+def _rounder(bf16_operands, operands):
+    if operands is None:
+        operands = "bf16" if bf16_operands else None
+    return {None: lambda a: a, "bf16": bf16_round, "f16": f16_round}[operands]
+
+
 def _sig(x):
     return 1.0 / (1.0 + np.exp(-x))
 
@@ -43,11 +57,12 @@ def _logsig(x):
     return np.minimum(x, 0) - np.log1p(np.exp(-np.abs(x)))
 
 
-def forward(wx, R, b, s0, cell, bf16_operands=False):
-    """Returns (history [S,B,T,N,D], caches). Arrays in their given float dtype."""
+def forward(wx, R, b, s0, cell, bf16_operands=False, operands=None):
+    """Returns (history [S,B,T,N,D], caches). Arrays in their given float dtype.
+    ``operands``: None, "bf16" or "f16" (``bf16_operands=True`` means "bf16")."""
     dt = wx.dtype.type
     B, T, _, N, D = wx.shape
-    rnd = bf16_round if bf16_operands else (lambda a: a)
+    rnd = _rounder(bf16_operands, operands)
     Rr = rnd(R).astype(dt)
     state = s0[:, :, 0].copy()
     hist, caches = [], []
@@ -100,16 +115,16 @@ def _tie_weights(a, b):
     return np.where(a > b, 1.0, np.where(a == b, 0.5, 0.0))
 
 
-def backward(wx, R, b, s0, cell, d_hist, d_last, bf16_operands=False):
+def backward(wx, R, b, s0, cell, d_hist, d_last, bf16_operands=False, operands=None):
     """Explicit backward. ``d_hist`` [S,B,T,N,D], ``d_last`` [S,B,1,N,D].
 
     Returns (dwx, dR, db, ds0) with the same shapes as the inputs.
     """
     dt = wx.dtype.type
     B, T, _, N, D = wx.shape
-    rnd = bf16_round if bf16_operands else (lambda a: a)
+    rnd = _rounder(bf16_operands, operands)
     Rr = rnd(R).astype(dt)
-    _, caches = forward(wx, R, b, s0, cell, bf16_operands)
+    _, caches = forward(wx, R, b, s0, cell, bf16_operands, operands)
     S = s0.shape[0]
     dwx = np.zeros_like(wx)
     dR = np.zeros_like(R)

@@ -94,12 +94,13 @@ def test_unsupported_widths(lib, D):
         ("lstm", 512, "bf16", True), ("gru", 768, "bf16", True), ("lstm", 768, "bf16", True),
         ("slstm", 576, "bf16", True), ("elman", 1024, "bf16", True), ("gru", 800, "bf16", False),
         ("lstm", 1024, "bf16", False), ("lstm", 512, "f32", True), ("gru", 768, "f32", False),
-        ("elman", 768, "f32", True),
+        ("elman", 768, "f32", True), ("lstm", 768, "f16", True), ("slstm", 256, "f16", True),
+        ("lstm", 1024, "f16", False),
     ],
 )
 def test_width_support(lib, cell, D, mma, ok):
     """The plan's register budget: which head widths each operand type supports."""
-    m = _lib.FRNN_MMA_BF16 if mma == "bf16" else _lib.FRNN_MMA_F32
+    m = {"bf16": _lib.FRNN_MMA_BF16, "f16": _lib.FRNN_MMA_F16, "f32": _lib.FRNN_MMA_F32}[mma]
     d = desc(cell=cell, B=16, T=8, N=1, D=D, mma=m)
     assert (lib.frnn_workspace_bytes(ctypes.byref(d), 0) > 0) == ok
 
@@ -172,7 +173,8 @@ def test_config_validation():
     with pytest.raises(ValueError):
         FlashRNNConfig(backend="vanilla")
     with pytest.raises(ValueError):
-        FlashRNNConfig(dtype="float16")
+        FlashRNNConfig(dtype="float64")
+    FlashRNNConfig(dtype="float16")
     for bad in (-1.0, float("nan"), float("inf")):
         with pytest.raises(ValueError, match="clipval"):
             FlashRNNConfig(gradient_recurrent_clipval=bad)

@@ -286,3 +286,58 @@ def test_rejects_invalid_contract():
     for args, kw, msg in cases:
         with pytest.raises(ValueError, match=msg):
             flashrnn_torch(*args, **kw)
+
+
+# ------------------------------------------------------- FP16 operand policy
+# The FP16 kernels follow FlashRNN2's FP16 contract (FP16 inputs, FP32 compute
+# and state; flashrnn/flashrnn2/state_contract.py:21-49): the policy of
+# fp32_state_bf16_mma with FP16 operands. Its oracle is the restatement's
+# ``recurrence`` with FP16 operand rounding; it is pinned here against the
+# explicit NumPy forward and hand-derived backward, whose FP16 rounding is
+# NumPy's own conversion.
+def f16_policy(wx, R, b, s0, cell):
+    from oracle.torch_restatement import recurrence
+
+    return recurrence(wx, R, b, s0, cell=cell, mma_dtype=torch.float16, recurrent_mma_dtype=torch.float16)
+
+
+@pytest.mark.parametrize("cell", list(SIZES))
+def test_f16_policy_equals_explicit(cell):
+    wx, R, b, s0 = rand_inputs(cell, B=3, T=6, N=2, D=5, dtype=torch.float32, seed=9)
+    hist, last = f16_policy(wx, R, b, s0, cell)
+    npy = [t.detach().numpy() for t in (wx, R, b, s0)]
+    ehist, _ = ne.forward(*npy, cell, operands="f16")
+    assert np.abs(hist.detach().numpy() - ehist).max() <= 2e-5
+    g = torch.Generator().manual_seed(10)
+    dh = torch.randn(hist.shape, generator=g)
+    dl = torch.randn(last.shape, generator=g)
+    grads = torch.autograd.grad((hist * dh).sum() + (last * dl).sum(), (wx, R, b, s0))
+    mine = ne.backward(*npy, cell, dh.numpy(), dl.numpy(), operands="f16")
+    for a, e in zip(mine, grads):
+        e = e.numpy()
+        assert np.abs(a - e).max() / np.abs(e).max() <= 1e-4
+
+
+def test_f16_policy_rounds_operands():
+    """The FP16 policy differs from the mathematical one by FP16 operand rounding only:
+    with R and every hidden state exactly representable in FP16 (R = 0, so h is the
+    pointwise cell of Wx + b) the two agree bitwise; with general R they differ."""
+    wx, R, b, s0 = rand_inputs("elman", B=2, T=4, N=1, D=3, dtype=torch.float32, seed=11)
+    with torch.no_grad():
+        Rz = torch.zeros_like(R)
+        s0z = torch.zeros_like(s0)
+    a, _ = f16_policy(wx, Rz, b, s0z, "elman")
+    e, _ = flashrnn_torch(wx, Rz, b, s0z, cell="elman")
+    assert torch.equal(a, e)
+    a, _ = f16_policy(wx, R, b, s0, "elman")
+    e, _ = flashrnn_torch(wx, R, b, s0, cell="elman")
+    assert 0 < (a - e).abs().max() < 1e-2
+
+
+def test_f16_round_is_rne():
+    from oracle.numpy_explicit import f16_round
+
+    x = np.array([1.0, 1.0 + 2**-11, 1.0 + 3 * 2**-11, 1.0 + 2**-12, -2.5, 65504.0], dtype=np.float32)
+    assert f16_round(x).tolist() == [1.0, 1.0, 1.0 + 4 * 2**-11, 1.0, -2.5, 65504.0]
+    t = torch.from_numpy(x).to(torch.float16).float().numpy()
+    assert (t == f16_round(x)).all()
