@@ -40,12 +40,12 @@ from .flashrnn import _IO, _MMA_OF, CELL_SIZES, _after_call, _drain_pending, _st
 from .prepared import KernelConfig, default_config
 
 
-def _flags(output_mode, snap32, cell, config, training):
+def _flags(output_mode, snap32, cell, config, training, v1=True):
     exchange = config.exchange or ("shared" if _state["xcd_shared"] else "xcd")
     flags = _lib.FRNN_TRAINING if training else 0
     flags |= _lib.FRNN_OUT_HIDDEN if output_mode != "full" else 0
     flags |= _lib.FRNN_SNAPSHOT_F32 if snap32 else 0
-    flags |= _lib.FRNN_SLSTM_V1GRAD if cell == "slstm" else 0
+    flags |= _lib.FRNN_SLSTM_V1GRAD if cell == "slstm" and v1 else 0
     flags |= _lib.FRNN_XCD_SHARED if exchange == "shared" else 0
     flags |= _lib.FRNN_TEST_UNREADY if _state["test_unready"] else 0
     return flags
@@ -53,7 +53,7 @@ def _flags(output_mode, snap32, cell, config, training):
 
 class _Recurrence(torch.autograd.Function):
     @staticmethod
-    def forward(ctx, wx, recurrent, bias, initial, cell, output_mode, snapshot_dtype, config):
+    def forward(ctx, wx, recurrent, bias, initial, cell, output_mode, snapshot_dtype, config, v1=True):
         _drain_pending()
         lib = _lib.load()
         B, T, _, N, D = wx.shape
@@ -61,7 +61,7 @@ class _Recurrence(torch.autograd.Function):
         dev = wx.device
         snap = wx.dtype if snapshot_dtype is None else snapshot_dtype
         training = torch.is_grad_enabled() or any(ctx.needs_input_grad[:4])
-        flags = _flags(output_mode, snap == torch.float32 and snap != wx.dtype, cell, config, training)
+        flags = _flags(output_mode, snap == torch.float32 and snap != wx.dtype, cell, config, training, v1)
         mma = _MMA_OF[wx.dtype]
         d = _lib.FrnnDesc(_lib.CELLS[cell], B, T, N, D, _IO[wx.dtype], _lib.FRNN_F32, mma, flags, 0.0, 0, 0)
         s0 = initial[:, :, 0].to(torch.float32).contiguous()  # exact; the carry is FP32
@@ -111,23 +111,29 @@ class _Recurrence(torch.autograd.Function):
                           stream)
         _lib.check(rc, "frnn_bwd")
         _after_call(ws)
-        return dwx, dR, db, ds0.unsqueeze(2).to(init_dtype), None, None, None, None
+        return dwx, dR, db, ds0.unsqueeze(2).to(init_dtype), None, None, None, None, None
 
 
 def recurrence(wx, recurrent, bias, initial, cell="lstm", *, output_mode="hidden", snapshot_dtype=None, config=None,
                sequence_context=None, backward_options=None):
     """Differentiable whole-call recurrence. Returns (output, FP32 final carry)."""
+    if sequence_context is not None and getattr(sequence_context, "step_offset", 0) > 0:
+        raise ValueError("a continuation chunk cannot be differentiated; run the whole logical call")
+    if backward_options:
+        raise ValueError("backward_options are tuning knobs of the reference's CUDA/Triton backwards; "
+                         "this backward has none")
+    return _recurrence(wx, recurrent, bias, initial, cell, output_mode, snapshot_dtype, config, v1=True)
+
+
+def _recurrence(wx, recurrent, bias, initial, cell, output_mode, snapshot_dtype, config, v1):
+    """``recurrence`` with the sLSTM gradient convention as a choice: v1 (FlashRNN2's
+    training) or exact (flashrnn_torch's, as ``flashrnn()`` uses)."""
     if cell not in CELL_SIZES:
         raise ValueError(f"unknown cell {cell!r}")
     if output_mode not in ("full", "hidden", "last"):
         raise ValueError("output mode must be full, hidden or last")
     if snapshot_dtype not in (None, wx.dtype, torch.float32):
         raise ValueError("snapshot dtype must be input dtype or FP32")
-    if sequence_context is not None and getattr(sequence_context, "step_offset", 0) > 0:
-        raise ValueError("a continuation chunk cannot be differentiated; run the whole logical call")
-    if backward_options:
-        raise ValueError("backward_options are tuning knobs of the reference's CUDA/Triton backwards; "
-                         "this backward has none")
     gr, gw, gt, S = CELL_SIZES[cell]
     if wx.ndim != 5:
         raise ValueError(f"expected Wx [B,T,{gw},H,D]")
@@ -157,7 +163,7 @@ def recurrence(wx, recurrent, bias, initial, cell="lstm", *, output_mode="hidden
         pad = Dp - D
         args = [F.pad(wx, (0, pad)), F.pad(recurrent, (0, pad, 0, pad)), F.pad(bias, (0, pad)),
                 F.pad(initial, (0, pad))]
-    out, final = _Recurrence.apply(*(t.contiguous() for t in args), cell, output_mode, snapshot_dtype, config)
+    out, final = _Recurrence.apply(*(t.contiguous() for t in args), cell, output_mode, snapshot_dtype, config, v1)
     if Dp != D:
         out, final = out[..., :D], final[..., :D]
     return out, final

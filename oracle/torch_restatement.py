@@ -298,3 +298,18 @@ def training_recurrence(
     hist = torch.stack(history, dim=2)
     out = hist if output_mode == "full" else (hist[0] if output_mode == "hidden" else hist[0][:, -1:])
     return out, state.unsqueeze(2)
+
+
+# ----------------------------------------------------------------------------
+# The layer around the path: input projection + recurrence. The reference
+# leaves the projection to the caller (``README.md:17``); its layer contract is
+# ``TorchLayer`` (``flashrnn/flashrnn2/torch_layer.py:14-80``): projection
+# weight [G,N,D,I] (``torch.nn``'s weight_ih per head, ``torch_layer.py:43-45``),
+# inputs [B,T,I] -> hidden history [B,T,N,D] and final states [S,B,1,N,D].
+def flashrnn_layer(inputs, input_weight, recurrent, bias, initial, *, cell="lstm", numerics="mathematical",
+                   wx_dtype=None):
+    """Returns (hidden [B,T,N,D], final [S,B,1,N,D]). ``wx_dtype``: the dtype the
+    projection's result is stored in before the recurrence reads it (None: not rounded)."""
+    wx = _round_through(torch.einsum("bti,gndi->btgnd", inputs, input_weight), wx_dtype)
+    hist, last = flashrnn_torch(wx, recurrent, bias, initial, cell=cell, numerics=numerics)
+    return hist[0], last
