@@ -188,7 +188,10 @@ struct Prof {
     const unsigned long long now = __builtin_amdgcn_s_memrealtime();
     if ((int)(threadIdx.x & 63) == slot) tv = now;
   }
-  __device__ __forceinline__ void flush_trace(unsigned long long* trace) {
+  // Slot 7 (stamp 7 of the first traced step, never stamped) carries the
+  // workgroup's (group, member) as group * 65536 + member.
+  __device__ __forceinline__ void flush_trace(unsigned long long* trace, const Team& tm) {
+    if ((threadIdx.x & 63) == 7) tv = (unsigned long long)tm.group * 65536ull + (unsigned long long)tm.member;
     if (tr && blockIdx.x < 128) trace[(blockIdx.x * 16 + (threadIdx.x >> 6)) * 64 + (threadIdx.x & 63)] = tv;
   }
   __device__ __forceinline__ void mark(int k) {
@@ -490,14 +493,20 @@ __device__ void fwd_io(const FwdArgs& a, const Team& tm, float* xring, float* os
         *reinterpret_cast<f32x4*>(a.save + save_index(p, NE, t, tm.wgi, v - S, tm.team, e0)) = x;
     }
   };
-  // Per iteration t: wait for the loads of step t+1; barrier t; drain step
-  // t-1; issue the loads of step t+P. VMEM operations issued after the loads
-  // of step t+1, at the top of iteration t (steady state): P-2 iterations of
-  // stores and loads.
+  // Per iteration t: wait for the loads of step t+1; barrier t; issue the
+  // loads of step t+P; drain step t-1. The HBM loads go out first, as early as
+  // the ring allows: the CU's vector-memory path returns data in order, so
+  // loads issued later would hold up the compute waves' exchange polls behind
+  // their HBM latency. VMEM operations issued after the loads of step t+1, at
+  // the top of iteration t (steady state, t >= P): the stores of the iteration
+  // that issued them, then P-2 iterations of loads and stores.
   static_assert(P >= 2, "prefetch distance");
   // stores per step: the policy's states (S, 1 or none in the loop) plus the saves when training
-  constexpr int kAfterTrain = (P - 2) * (GW + NV), kAfterTrainHidden = (P - 2) * (GW + 1 + NSAVE);
-  constexpr int kAfterFull = (P - 2) * (GW + S), kAfterHidden = (P - 2) * (GW + 1), kAfterLast = (P - 2) * GW;
+  constexpr int kStTrain = NV, kStTrainHidden = 1 + NSAVE, kStFull = S, kStHidden = 1;
+  constexpr int kAfterTrain = kStTrain + (P - 2) * (GW + kStTrain);
+  constexpr int kAfterTrainHidden = kStTrainHidden + (P - 2) * (GW + kStTrainHidden);
+  constexpr int kAfterFull = kStFull + (P - 2) * (GW + kStFull);
+  constexpr int kAfterHidden = kStHidden + (P - 2) * (GW + kStHidden), kAfterLast = (P - 2) * GW;
 
   Prof prof;
   prof.init(a.prof != nullptr && blockIdx.x == 0, a.prof != nullptr);
@@ -505,7 +514,7 @@ __device__ void fwd_io(const FwdArgs& a, const Team& tm, float* xring, float* os
   wait_vm<0>();
   lds_barrier();  // Wx_0 in its slot
   for (int t = 0; t < T; ++t) {
-    if (t + 1 >= P && t + P <= T) {
+    if (t >= P && t + P <= T) {
       if (training && mode == 0) wait_vm<kAfterTrain>();
       else if (training) wait_vm<kAfterTrainHidden>();
       else if (mode == 0) wait_vm<kAfterFull>();
@@ -521,10 +530,10 @@ __device__ void fwd_io(const FwdArgs& a, const Team& tm, float* xring, float* os
     lds_barrier();  // step t: Wx_{t+1} in its slot; outputs of step t-1 staged
     prof.mark(2);
     prof.stamp(t, 2);
-    if (t >= 1) store_out(t - 1, ost + ((t - 1) & 1) * NV * NE);
     // slot (t+P) % kFwdRing held step t-1, which every owner finished reading
     // before barrier t-1
     if (t + P < T) load_wx(t + P);
+    if (t >= 1) store_out(t - 1, ost + ((t - 1) & 1) * NV * NE);
     prof.mark(3);
     prof.stamp(t, 3);
   }
@@ -532,7 +541,7 @@ __device__ void fwd_io(const FwdArgs& a, const Team& tm, float* xring, float* os
   store_out(T - 1, ost + ((T - 1) & 1) * NV * NE);
   prof.acc[5] = T;
   prof.flush(a.prof);
-  if (a.prof) prof.flush_trace(a.prof + 256);
+  if (a.prof) prof.flush_trace(a.prof + 256, tm);
 }
 
 template <int CELL, int MMA, int KTW, int NB, int NDT, int KSC>
@@ -755,7 +764,7 @@ __global__ void __launch_bounds__(64 * (KSC + 1) * NDT) fwd_kernel(FwdArgs a) {
   }
   prof.acc[5] = T;
   prof.flush(a.prof);
-  if (a.prof) prof.flush_trace(a.prof + 256);
+  if (a.prof) prof.flush_trace(a.prof + 256, tm);
 }
 
 // ===================================================================== backward
@@ -865,7 +874,7 @@ __device__ void bwd_io(const BwdArgs& a, const Team& tm, float* iring, float* os
   }
   prof.acc[5] = T;
   prof.flush(a.prof ? a.prof + 128 : nullptr);
-  if (a.prof) prof.flush_trace(a.prof + 256 + 128 * 16 * 64);
+  if (a.prof) prof.flush_trace(a.prof + 256 + 128 * 16 * 64, tm);
 }
 
 template <int CELL, int MMA, int KTW, int NB, int NDT, int KSC>
@@ -1104,7 +1113,7 @@ __global__ void __launch_bounds__(64 * (KSC + 1) * NDT) bwd_kernel(BwdArgs a) {
   }
   prof.acc[5] = T;
   prof.flush(a.prof ? a.prof + 128 : nullptr);
-  if (a.prof) prof.flush_trace(a.prof + 256 + 128 * 16 * 64);
+  if (a.prof) prof.flush_trace(a.prof + 256 + 128 * 16 * 64, tm);
 }
 
 }  // namespace frnn
