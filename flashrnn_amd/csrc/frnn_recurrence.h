@@ -181,6 +181,13 @@ struct Prof {
     for (int i = 0; i < 8; ++i) acc[i] = 0;
     t = on ? clock64() : 0;
   }
+  // Record a value (not a time) in slot k of a traced step.
+  __device__ __forceinline__ void put(int step, int k, unsigned long long v) {
+    if (!tr) return;
+    const int slot = (step - kTraceT0) * 8 + k;
+    if (slot < 0 || slot >= 64) return;
+    if ((int)(threadIdx.x & 63) == slot) tv = v;
+  }
   __device__ __forceinline__ void stamp(int step, int k) {
     if (!tr) return;
     const int slot = (step - kTraceT0) * 8 + k;
@@ -426,12 +433,19 @@ __device__ __forceinline__ void wait_vm() {
   __builtin_amdgcn_s_waitcnt((n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
-// Wx value of gate g for owned element (slab row r, unit d of the tile) from
-// a raw ring slot (see the LDS layout above).
-__device__ __forceinline__ float ring_x(const float* slot, int g, int r, int d, int dt) {
-  if (dt == DT_F32) return slot[(g * 64 + r * 4 + (d >> 2)) * 4 + (d & 3)];
-  const unsigned short* h = reinterpret_cast<const unsigned short*>(slot);
-  return h16_to_f32(h[(g * 64 + r * 4 + (d >> 3) * 2) * 8 + (d & 7)], dt);
+// Wx of gate g for owned element (slab row r, unit d of the tile) in a raw
+// ring slot (see the LDS layout above): the 32-bit word that holds it, read
+// raw so the owners issue every gate's read at once and convert only at the
+// next step's cell, and the value from that word.
+__device__ __forceinline__ int ring_word(int g, int r, int d, int dt) {
+  return dt == DT_F32 ? (g * 64 + r * 4 + (d >> 2)) * 4 + (d & 3) : (g * 64 + r * 4 + (d >> 3) * 2) * 4 + ((d & 7) >> 1);
+}
+// Branch-free in the runtime dtype: every form is computed and one selected.
+__device__ __forceinline__ float ring_val(uint32_t w, int d, int dt) {
+  const uint32_t h = (w >> ((d & 1) * 16)) & 0xffffu;
+  const float vf = u2f(w), vb = u2f(h << 16), vh = f16_to_f32(h);
+  const float v16 = dt == DT_F16 ? vh : vb;
+  return dt == DT_F32 ? vf : v16;
 }
 
 // I/O wave of a team. Wx of step u is loaded straight into ring slot
@@ -653,13 +667,19 @@ __global__ void __launch_bounds__(64 * (KSC + 1) * NDT) fwd_kernel(FwdArgs a) {
   __builtin_amdgcn_s_waitcnt(0);
   lds_barrier();  // Wx_0 in its slot
   // Wx of the next step, read from the ring right after each cell
-  float xnext[EPLMAX][GW];
+  // (raw words: the reads are waited for at the next barrier, not here)
+  uint32_t xnext[EPLMAX][GW];
+  int xw[EPLMAX][GW];
+#pragma unroll
+  for (int s = 0; s < EPLMAX; ++s)
+#pragma unroll
+    for (int g = 0; g < GW; ++g) xw[s][g] = ring_word(g, el[s].bl & 15, el[s].d & 15, p.dt_io);
   auto read_x = [&](int u) {
-    const float* xr = xring + (long)(u % kFwdRing) * RING;
+    const uint32_t* xr = reinterpret_cast<const uint32_t*>(xring + (long)(u % kFwdRing) * RING);
 #pragma unroll
     for (int s = 0; s < EPLMAX; ++s)
 #pragma unroll
-      for (int g = 0; g < GW; ++g) xnext[s][g] = el[s].real ? ring_x(xr, g, el[s].bl, el[s].d & 15, p.dt_io) : 0.f;
+      for (int g = 0; g < GW; ++g) xnext[s][g] = xr[xw[s][g]];
   };
   read_x(0);
   bool abort = false;
@@ -717,7 +737,7 @@ __global__ void __launch_bounds__(64 * (KSC + 1) * NDT) fwd_kernel(FwdArgs a) {
       for (int w2 = 0; w2 < KS; ++w2) part[w2] = *reinterpret_cast<const f32x4*>(rp + w2 * NB * RED_F + src);
       float xcur[GW];
 #pragma unroll
-      for (int g = 0; g < GW; ++g) xcur[g] = xnext[s][g];
+      for (int g = 0; g < GW; ++g) xcur[g] = el[s].real ? ring_val(xnext[s][g], el[s].d, p.dt_io) : 0.f;
       float ry[GR];
 #pragma unroll
       for (int g = 0; g < GR; ++g) {
