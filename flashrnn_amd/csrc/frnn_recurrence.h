@@ -934,7 +934,15 @@ __global__ void __launch_bounds__(64 * (KSC + 1) * NDT) bwd_kernel(BwdArgs a) {
   }
 
   Xchg xc;
-  xc.base = a.xbuf;
+  {
+    // Held in VGPRs (backward only: measured slower in the forward): under
+    // SGPR pressure the compiler otherwise reloads the pointer from the kernel
+    // arguments inside the time loop, and the scalar load's wait lands in
+    // front of the exchange stores.
+    uintptr_t xb = reinterpret_cast<uintptr_t>(a.xbuf);
+    asm("" : "+v"(xb));
+    xc.base = reinterpret_cast<char*>(xb);
+  }
   xc.shared_xcd = (p.flags & 2) ? 1 : 0;
   xc.rsrc = __builtin_amdgcn_make_buffer_rsrc(a.xbuf, 0, (int)a.xbytes, 0x00020000);
 
