@@ -50,6 +50,7 @@ EXPORTS = (
     "frnn_status",
     "frnn_strerror",
     "frnn_set_spin_limit",
+    "frnn_set_scouts",
     "frnn_timing_enable",
     "frnn_timing_read",
     "frnn_set_phase_profile",
@@ -86,6 +87,8 @@ def load(path: str | os.PathLike | None = None) -> ctypes.CDLL:
     lib.frnn_strerror.restype = ctypes.c_char_p
     lib.frnn_set_spin_limit.argtypes = [ctypes.c_uint32]
     lib.frnn_set_spin_limit.restype = None
+    lib.frnn_set_scouts.argtypes = [i32]
+    lib.frnn_set_scouts.restype = None
     lib.frnn_timing_enable.argtypes = [i32]
     lib.frnn_timing_enable.restype = None
     lib.frnn_timing_read.argtypes = [ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_int32)]

@@ -21,6 +21,11 @@ using frnn::Plan;
 
 constexpr uint32_t kDefaultSpinLimit = 1u << 22;
 std::atomic<uint32_t> g_spin_limit{kDefaultSpinLimit};
+// FRNN_NO_SCOUT=1 (environment, read once): no L2-prefetch workgroups in the backward.
+std::atomic<bool> g_no_scout{[] {
+  const char* e = std::getenv("FRNN_NO_SCOUT");
+  return e && *e && *e != '0';
+}()};
 std::atomic<unsigned long long*> g_phase_prof{nullptr};
 
 // ---- optional kernel timing (frnn_timing_enable / frnn_timing_read)
@@ -118,7 +123,9 @@ bool fits(const Plan& p, int ks, bool forward) {
 void set_groups(Plan* p, int g0, int n) {
   p->g0 = g0;
   p->gcount = n;
-  p->grid = (p->flags & FRNN_XCD_SHARED) ? n * p->wpg : frnn::kXcds * p->wpg * ((n + frnn::kXcds - 1) / frnn::kXcds);
+  p->grid = (p->flags & FRNN_XCD_SHARED)
+                ? n * p->wpg
+                : frnn::kXcds * (p->wpg + ((p->flags & frnn::kFlagScout) ? 1 : 0)) * ((n + frnn::kXcds - 1) / frnn::kXcds);
 }
 
 int make_plan(const frnn_desc* d, Plan* p) {
@@ -237,6 +244,16 @@ int set_lds_limit(const void* fn, size_t lds) {
   return FRNN_OK;
 }
 
+// Workgroups of the kernel one CU holds at once (0 on error).
+int blocks_per_cu(const void* fn, int block, size_t lds) {
+  int per_cu = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, block, lds) != hipSuccess) {
+    (void)hipGetLastError();
+    return 0;
+  }
+  return per_cu;
+}
+
 // The persistent kernels need every workgroup of a group resident at once
 // (groups never wait on each other). Return in *per_launch how many groups one
 // launch may hold: what the GPU holds placement-free, or with every group on
@@ -253,7 +270,7 @@ int groups_per_launch(const Plan& p, const void* fn, int block, size_t lds, int*
   if (p.flags & FRNN_XCD_SHARED)
     g = (long long)cus * per_cu / p.wpg;
   else
-    g = (long long)frnn::kXcds * ((long long)(cus / frnn::kXcds) * per_cu / p.wpg);
+    g = (long long)frnn::kXcds * ((long long)(cus / frnn::kXcds) * per_cu / (p.wpg + ((p.flags & frnn::kFlagScout) ? 1 : 0)));
   if (g < 1) return FRNN_E_UNSUPPORTED;
   *per_launch = (int)std::min<long long>(g, p.ngroups);
   return FRNN_OK;
@@ -392,6 +409,20 @@ int frnn_bwd(const frnn_desc* d, const void* R, const void* s0, const void* stat
   int per_launch = 0;
   if ((rc = set_lds_limit(fn, lds)) != FRNN_OK) return rc;
   if ((rc = groups_per_launch(p, fn, block, lds, &per_launch)) != FRNN_OK) return rc;
+  // Scouts (L2 prefetch of the I/O waves' inputs) where they cost no extra
+  // launch and have a CU to themselves (one workgroup per CU: a scout's HBM
+  // loads would otherwise hold up the polls of a member on its CU), with the
+  // XCD-local exchange and a recurrent exchange to pace them by.
+  if (!(p.flags & (FRNN_XCD_SHARED | FRNN_GRAD_CUT)) && !g_no_scout.load()) {
+    Plan ps = p;
+    ps.flags |= frnn::kFlagScout;
+    int per_scout = 0;
+    if (blocks_per_cu(fn, block, lds) == 1 && groups_per_launch(ps, fn, block, lds, &per_scout) == FRNN_OK &&
+        (p.ngroups + per_scout - 1) / per_scout == (p.ngroups + per_launch - 1) / per_launch) {
+      a.p.flags |= frnn::kFlagScout;
+      per_launch = per_scout;
+    }
+  }
   hipEvent_t t0;
   bool timed = timing_begin(st, &t0);
   rc = launch_groups(&a.p, fn, block, lds, &a, per_launch, st);
@@ -471,5 +502,7 @@ void frnn_set_phase_profile(void* device_words) {
 }
 
 void frnn_set_spin_limit(uint32_t polls) { g_spin_limit.store(polls ? polls : kDefaultSpinLimit); }
+
+void frnn_set_scouts(int enable) { g_no_scout.store(enable == 0); }
 
 }  // extern "C"

@@ -19,6 +19,10 @@ constexpr int kMaxNFB = 32;   // max 32-wide k-tiles per wave (backward)
 // Plan flags (the C ABI's frnn_flags)
 constexpr int kFlagTraining = 1, kFlagShared = 2, kFlagCut = 4, kFlagClip = 8, kFlagUnready = 16;
 constexpr int kFlagOutHidden = 32, kFlagOutLast = 64, kFlagSnapF32 = 128, kFlagV1Grad = 256;
+// Launch-internal flag (never set by a caller): one more workgroup per group
+// (XCD-local mode, backward), the group's scout, that touches the inputs of
+// later steps so they wait in the XCD's L2.
+constexpr int kFlagScout = 1 << 20;
 
 struct Plan {
   int cell, B, T, N, D;
@@ -60,6 +64,12 @@ struct Plan {
 //  * XCD-local exchange: wg is the workgroup's claim on its XCD (the
 //    workgroups that run on XCD x number themselves 0, 1, ... in arrival
 //    order), and groups x, x + 8, x + 16, ... of the launch live on XCD x.
+//    With scouts, the claims after the last member's go to the scouts of the
+//    XCD's groups in the same order (member == wpg): they arrive last, so a
+//    scout never takes a slot a member needs.
+// SCOUTS: decode scout claims too (the backward kernel only; the forward
+// kernel's decode stays the minimal one, which measured faster there).
+template <bool SCOUTS = false>
 #if defined(__HIPCC__)
 __host__ __device__
 #endif
@@ -69,9 +79,15 @@ inline bool wg_decode(const Plan& p, int wg, int xcd, int* group, int* member) {
     local = wg / p.wpg;
     *member = wg % p.wpg;
   } else {
-    const int slot = wg / p.wpg;
+    local = (wg / p.wpg) * kXcds + xcd;
     *member = wg % p.wpg;
-    local = slot * kXcds + xcd;
+    if constexpr (SCOUTS) {
+      const int spx = (p.gcount + kXcds - 1) / kXcds;  // groups per XCD
+      if ((p.flags & kFlagScout) && wg >= spx * p.wpg) {
+        *member = p.wpg;
+        local = (wg - spx * p.wpg) * kXcds + xcd;
+      }
+    }
   }
   *group = p.g0 + local;
   return local < p.gcount;

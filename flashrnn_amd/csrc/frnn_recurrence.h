@@ -98,6 +98,7 @@ struct Team {
 // The claim is broadcast through the first word of the kernel's dynamic LDS
 // (a static __shared__ variable would shift the dynamic area off its 16-byte
 // alignment), which is free again after the second barrier.
+template <bool SCOUTS = false>
 __device__ __forceinline__ bool team_setup(const Plan& p, Team& tm, uint32_t* claim, uint32_t* status, int KS,
                                            float* lds) {
   int wg = blockIdx.x, xcd = 0;
@@ -117,7 +118,7 @@ __device__ __forceinline__ bool team_setup(const Plan& p, Team& tm, uint32_t* cl
     }
     wg = (int)slot;
   }
-  if (!wg_decode(p, wg, xcd, &tm.group, &tm.member)) return false;
+  if (!wg_decode<SCOUTS>(p, wg, xcd, &tm.group, &tm.member)) return false;
   tm.lane = threadIdx.x & 63;
   tm.w = threadIdx.x >> 6;
   tm.team = tm.w / (KS + 1);
@@ -897,6 +898,76 @@ __device__ void bwd_io(const BwdArgs& a, const Team& tm, float* iring, float* os
   if (a.prof) prof.flush_trace(a.prof + 256 + 128 * 16 * 64, tm);
 }
 
+// Scout of a group (backward; one extra workgroup on the group's XCD): it
+// touches the lines the group's I/O waves will load a few iterations later
+// (state cotangents of the real batch rows, saved values), so those loads hit
+// the XCD's L2 instead of HBM. A CU's vector memory returns data in issue
+// order, so an HBM load in an I/O wave holds up every exchange poll of its CU
+// issued after it; the scout, on a CU of its own, takes that latency instead.
+// The touches are LDS-DMA loads (no registers in flight; the LDS content is
+// never read). The scout paces itself by the exchange word that member 0
+// publishes each iteration; nothing waits for it, and every wait of its own is
+// bounded (spin limit, sticky status), so it always finishes.
+constexpr int kScoutLead = 6;  // iteration the scout touches when iteration j is published: j + kScoutLead
+template <int CELL, int MMA>
+__device__ void bwd_scout(const BwdArgs& a, const Team& tm, float* lds) {
+  using CS = CellShape<CELL>;
+  constexpr int S = CS::S, GR = CS::GR;
+  const Plan& p = a.p;
+  const int T = p.T, N = p.N, D = p.D, B = p.B, NE = p.NB * 256;
+  const int nst = a.d_states ? ((p.flags & kFlagOutHidden) ? 1 : S) : 0;
+  const int esz = p.dt_out == DT_F32 ? 4 : 2;
+  const int b0 = tm.slab * p.BS, nreal = min(p.BS, B - b0);
+  const int row_bytes = D * esz, lpr = (row_bytes + 127) / 128 + 1;  // lines of one row (+1: unaligned rows)
+  const int nd = nst * nreal * lpr;                                    // state-cotangent touches
+  const int ns = p.wpg * p.nsave * p.NDT * p.NB * 8;                   // save touches (8 lines per 16-row tile)
+  auto lptr = (__attribute__((address_space(3))) void*)(lds + (threadIdx.x >> 6) * 64);
+  auto touch = [&](int it) {
+    const int t = T - 1 - it;
+    for (int i = threadIdx.x; i < nd + ns; i += blockDim.x) {
+      const char* src = nullptr;
+      if (i < nd) {
+        const int k = i / (nreal * lpr), r = (i / lpr) % nreal, l = i % lpr;
+        const long e0 = ((((long)k * B + b0 + r) * T + t) * N + tm.n) * D;
+        src = static_cast<const char*>(a.d_states) + e0 * esz + min(128 * l, row_bytes - 4);
+      } else {
+        const int j = i - nd, l = j & 7, bt = (j >> 3) % p.NB, rest = (j >> 3) / p.NB;
+        const int team = rest % p.NDT, v = (rest / p.NDT) % p.nsave, m = rest / (p.NDT * p.nsave);
+        const int rows = min(max(nreal - bt * 16, 0), 16);  // real rows of this 16-row tile
+        if (2 * l < rows)  // a 128-byte line holds two rows of 16 units
+          src = reinterpret_cast<const char*>(a.save + save_index(p, NE, t, tm.group * p.wpg + m, v, team, bt * 256) +
+                                              32 * l);
+      }
+      if (src) __builtin_amdgcn_global_load_lds(src, lptr, 4, 0, 0);
+    }
+  };
+  // the word of (row 0, k 0) of the group's table, parity by parity
+  const char* xw = a.xbuf + (long)tm.group * p.BS * GR * D * (MMA == MMA_F32 ? 8 : 4);
+  const long xpar_b = (long)p.ngroups * p.BS * GR * D * (MMA == MMA_F32 ? 8 : 4);
+  auto published = [&](int it) {
+    const char* w = xw + (it & 1) * xpar_b;
+    uint32_t tag;
+    if constexpr (MMA == MMA_F32) tag = __hip_atomic_load(reinterpret_cast<const uint32_t*>(w) + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    else tag = __hip_atomic_load(reinterpret_cast<const uint32_t*>(w), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) & 3u;
+    return tag == step_tag(it);
+  };
+  // Every wave paces itself (a barrier-paced variant measured slower).
+  for (int x = 3; x < kScoutLead && x < T; ++x) touch(x);
+  uint32_t spins = 0;
+  bool live = true;
+  for (int j = 0; live && j + kScoutLead < T; ++j) {
+    while (!published(j)) {
+      __builtin_amdgcn_s_sleep(2);
+      if (++spins >= a.spin_limit || ((spins & 255u) == 0 && load_status(a.status) != 0)) {
+        live = false;
+        break;
+      }
+    }
+    if (live) touch(j + kScoutLead);
+  }
+  __builtin_amdgcn_s_waitcnt(0);
+}
+
 template <int CELL, int MMA, int KTW, int NB, int NDT, int KSC>
 __global__ void __launch_bounds__(64 * (KSC + 1) * NDT) bwd_kernel(BwdArgs a) {
   using CS = CellShape<CELL>;
@@ -908,7 +979,11 @@ __global__ void __launch_bounds__(64 * (KSC + 1) * NDT) bwd_kernel(BwdArgs a) {
   const Plan& p = a.p;
   extern __shared__ float lds[];
   Team tm;
-  if (!team_setup(p, tm, a.claim, a.status, KSC, lds)) return;
+  if (!team_setup<true>(p, tm, a.claim, a.status, KSC, lds)) return;
+  if (tm.member == p.wpg) {  // the group's scout
+    bwd_scout<CELL, MMA>(a, tm, lds);
+    return;
+  }
   const int D = p.D, B = p.B, N = p.N, T = p.T;
   const int GD = GR * D;
   const bool cut = (p.flags & kFlagCut) != 0;

@@ -183,6 +183,13 @@ void frnn_set_phase_profile(void* device_words);
  * A tiny value forces FRNN_E_TIMEOUT from the host without faulting. */
 void frnn_set_spin_limit(uint32_t polls);
 
+/* Tuning hook, no counterpart in the reference: enable (1, the default unless the
+ * environment sets FRNN_NO_SCOUT=1) or disable (0) the backward's scouts, one extra
+ * workgroup per group that pulls the inputs of later steps into the L2 of the group's
+ * XCD. They change timing only, never results; they are used only where they cost no
+ * extra launch and get a CU to themselves. */
+void frnn_set_scouts(int enable);
+
 #ifdef __cplusplus
 }
 #endif

@@ -113,3 +113,26 @@ def test_odd_width_is_padded():
     actual, expected = run_pair("lstm", 2, 5, 2, 20, "float32", seed=3)
     for a, e in zip(actual, expected):
         assert rel(a, e) <= 1e-4
+
+
+@pytest.mark.parametrize("cell,B", [("lstm", 8), ("lstm", 16), ("slstm", 16)])
+def test_scouts_change_timing_only(cell, B):
+    """The backward's L2-prefetch workgroups (scouts) leave every output bitwise unchanged."""
+    from flashrnn_amd import _lib, flashrnn, set_strict
+
+    set_strict(True)
+    cpu, dh, dl = make(cell, B, 64, 2, 256, seed=5)
+    lib = _lib.load()
+    outs = []
+    try:
+        for on in (1, 0):
+            lib.frnn_set_scouts(on)
+            gl = [t.to("cuda", torch.bfloat16).requires_grad_() for t in cpu]
+            ah, al = flashrnn(*gl, function=cell, dtype="bfloat16")
+            ag = torch.autograd.grad((ah.float() * dh.cuda()).sum() + (al.float() * dl.cuda()).sum(), gl)
+            torch.cuda.synchronize()
+            outs.append([t.detach().cpu() for t in (ah, al, *ag)])
+    finally:
+        lib.frnn_set_scouts(1)
+    for a, b in zip(*outs):
+        assert torch.equal(a, b)
