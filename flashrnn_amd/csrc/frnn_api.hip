@@ -123,9 +123,9 @@ bool fits(const Plan& p, int ks, bool forward) {
 void set_groups(Plan* p, int g0, int n) {
   p->g0 = g0;
   p->gcount = n;
-  p->grid = (p->flags & FRNN_XCD_SHARED)
-                ? n * p->wpg
-                : frnn::kXcds * (p->wpg + ((p->flags & frnn::kFlagScout) ? 1 : 0)) * ((n + frnn::kXcds - 1) / frnn::kXcds);
+  p->grid = (p->flags & FRNN_XCD_SHARED) ? n * p->wpg
+                                          : frnn::kXcds * p->wpg * ((n + frnn::kXcds - 1) / frnn::kXcds) +
+                                                frnn::scout_blocks(*p);
 }
 
 int make_plan(const frnn_desc* d, Plan* p) {
@@ -211,7 +211,8 @@ int make_plan(const frnn_desc* d, Plan* p) {
   p->save_bytes = align_up(p->save_floats * 4);
   // workspaces: status word at 0, exchange at 256
   p->off_x = kAlign;
-  const long long nclaim = (long long)p->ngroups * frnn::kXcds * 4;  // by a launch's first group
+  // by a launch's first group: the members' counters, then the scouts'
+  const long long nclaim = 2LL * p->ngroups * frnn::kXcds * 4;
   p->off_claim_f = align_up(p->off_x + 2 * p->xwords_fwd * wsz);
   p->ws_fwd = align_up(p->off_claim_f + nclaim);
   p->off_claim_b = align_up(p->off_x + 2 * p->xwords_bwd * wsz);
@@ -274,6 +275,29 @@ int groups_per_launch(const Plan& p, const void* fn, int block, size_t lds, int*
   if (g < 1) return FRNN_E_UNSUPPORTED;
   *per_launch = (int)std::min<long long>(g, p.ngroups);
   return FRNN_OK;
+}
+
+// Scouts (L2 prefetch of the I/O waves' inputs, one workgroup per group) where
+// they cost no extra launch and have a CU to themselves, with the XCD-local
+// exchange and a recurrent exchange to pace them by. One workgroup per CU is
+// forced, where needed, by asking for more dynamic LDS than half a CU holds: a
+// scout's HBM loads would otherwise hold up the polls of a member on its CU
+// (and two members on one CU hold up each other's). Sets kFlagScout in the
+// launch plan *ap, the groups per launch and the dynamic LDS of the launch.
+void use_scouts(const Plan& p, const void* fn, int block, size_t* lds, Plan* ap, int* per_launch) {
+  if ((p.flags & (FRNN_XCD_SHARED | FRNN_GRAD_CUT)) || g_no_scout.load()) return;
+  constexpr size_t kHalfCu = 80 * 1024;
+  const size_t lds1 = *lds > kHalfCu ? *lds : kHalfCu + 1024;
+  if (set_lds_limit(fn, lds1) != FRNN_OK || blocks_per_cu(fn, block, lds1) != 1) return;
+  Plan ps = p;
+  ps.flags |= frnn::kFlagScout;
+  int per_scout = 0;
+  if (groups_per_launch(ps, fn, block, lds1, &per_scout) == FRNN_OK &&
+      (p.ngroups + per_scout - 1) / per_scout == (p.ngroups + *per_launch - 1) / *per_launch) {
+    ap->flags |= frnn::kFlagScout;
+    *per_launch = per_scout;
+    *lds = lds1;
+  }
 }
 
 // Launch the persistent kernel over all groups in as few launches as residency
@@ -360,11 +384,12 @@ int frnn_fwd(const frnn_desc* d, const void* wx, const void* R, const void* b, c
   a.status = reinterpret_cast<uint32_t*>(w);
   a.spin_limit = g_spin_limit.load();
   a.prof = g_phase_prof.load();
-  const size_t lds = (size_t)p.NDT * frnn::recurrence_lds_floats(p.cell, true, p.KS) * sizeof(float);
+  size_t lds = (size_t)p.NDT * frnn::recurrence_lds_floats(p.cell, true, p.KS) * sizeof(float);
   const int block = 64 * p.NDT * (p.KS + 1);
   int per_launch = 0;
   if ((rc = set_lds_limit(fn, lds)) != FRNN_OK) return rc;
   if ((rc = groups_per_launch(p, fn, block, lds, &per_launch)) != FRNN_OK) return rc;
+  use_scouts(p, fn, block, &lds, &a.p, &per_launch);
   hipEvent_t t0;
   const bool timed = timing_begin(st, &t0);
   rc = launch_groups(&a.p, fn, block, lds, &a, per_launch, st);
@@ -404,25 +429,12 @@ int frnn_bwd(const frnn_desc* d, const void* R, const void* s0, const void* stat
   a.status = reinterpret_cast<uint32_t*>(w);
   a.spin_limit = g_spin_limit.load();
   a.prof = g_phase_prof.load();
-  const size_t lds = (size_t)p.NDT * frnn::recurrence_lds_floats(p.cell, false, p.KSB) * sizeof(float);
+  size_t lds = (size_t)p.NDT * frnn::recurrence_lds_floats(p.cell, false, p.KSB) * sizeof(float);
   const int block = 64 * p.NDT * (p.KSB + 1);
   int per_launch = 0;
   if ((rc = set_lds_limit(fn, lds)) != FRNN_OK) return rc;
   if ((rc = groups_per_launch(p, fn, block, lds, &per_launch)) != FRNN_OK) return rc;
-  // Scouts (L2 prefetch of the I/O waves' inputs) where they cost no extra
-  // launch and have a CU to themselves (one workgroup per CU: a scout's HBM
-  // loads would otherwise hold up the polls of a member on its CU), with the
-  // XCD-local exchange and a recurrent exchange to pace them by.
-  if (!(p.flags & (FRNN_XCD_SHARED | FRNN_GRAD_CUT)) && !g_no_scout.load()) {
-    Plan ps = p;
-    ps.flags |= frnn::kFlagScout;
-    int per_scout = 0;
-    if (blocks_per_cu(fn, block, lds) == 1 && groups_per_launch(ps, fn, block, lds, &per_scout) == FRNN_OK &&
-        (p.ngroups + per_scout - 1) / per_scout == (p.ngroups + per_launch - 1) / per_launch) {
-      a.p.flags |= frnn::kFlagScout;
-      per_launch = per_scout;
-    }
-  }
+  use_scouts(p, fn, block, &lds, &a.p, &per_launch);
   hipEvent_t t0;
   bool timed = timing_begin(st, &t0);
   rc = launch_groups(&a.p, fn, block, lds, &a, per_launch, st);

@@ -64,12 +64,6 @@ struct Plan {
 //  * XCD-local exchange: wg is the workgroup's claim on its XCD (the
 //    workgroups that run on XCD x number themselves 0, 1, ... in arrival
 //    order), and groups x, x + 8, x + 16, ... of the launch live on XCD x.
-//    With scouts, the claims after the last member's go to the scouts of the
-//    XCD's groups in the same order (member == wpg): they arrive last, so a
-//    scout never takes a slot a member needs.
-// SCOUTS: decode scout claims too (the backward kernel only; the forward
-// kernel's decode stays the minimal one, which measured faster there).
-template <bool SCOUTS = false>
 #if defined(__HIPCC__)
 __host__ __device__
 #endif
@@ -79,18 +73,22 @@ inline bool wg_decode(const Plan& p, int wg, int xcd, int* group, int* member) {
     local = wg / p.wpg;
     *member = wg % p.wpg;
   } else {
-    local = (wg / p.wpg) * kXcds + xcd;
+    const int slot = wg / p.wpg;
     *member = wg % p.wpg;
-    if constexpr (SCOUTS) {
-      const int spx = (p.gcount + kXcds - 1) / kXcds;  // groups per XCD
-      if ((p.flags & kFlagScout) && wg >= spx * p.wpg) {
-        *member = p.wpg;
-        local = (wg - spx * p.wpg) * kXcds + xcd;
-      }
-    }
+    local = slot * kXcds + xcd;
   }
   *group = p.g0 + local;
   return local < p.gcount;
+}
+
+// Scouts (kFlagScout, XCD-local exchange only) are the last 8 * ceil(gcount / 8)
+// workgroups of a launch's grid, after the members' slots; each claims, on its
+// own counters, the next group of the XCD it runs on.
+#if defined(__HIPCC__)
+__host__ __device__
+#endif
+inline int scout_blocks(const Plan& p) {
+  return (p.flags & kFlagScout) ? kXcds * ((p.gcount + kXcds - 1) / kXcds) : 0;
 }
 
 }  // namespace frnn

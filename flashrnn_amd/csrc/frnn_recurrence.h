@@ -98,7 +98,6 @@ struct Team {
 // The claim is broadcast through the first word of the kernel's dynamic LDS
 // (a static __shared__ variable would shift the dynamic area off its 16-byte
 // alignment), which is free again after the second barrier.
-template <bool SCOUTS = false>
 __device__ __forceinline__ bool team_setup(const Plan& p, Team& tm, uint32_t* claim, uint32_t* status, int KS,
                                            float* lds) {
   int wg = blockIdx.x, xcd = 0;
@@ -112,13 +111,13 @@ __device__ __forceinline__ bool team_setup(const Plan& p, Team& tm, uint32_t* cl
     __syncthreads();
     const uint32_t slot = *s_slot;
     __syncthreads();
-    if (slot >= (uint32_t)(p.grid / kXcds)) {
+    if (slot >= (uint32_t)((p.grid - scout_blocks(p)) / kXcds)) {
       if (threadIdx.x == 0) raise_status(status, ST_PLACEMENT);
       return false;  // the whole workgroup leaves together
     }
     wg = (int)slot;
   }
-  if (!wg_decode<SCOUTS>(p, wg, xcd, &tm.group, &tm.member)) return false;
+  if (!wg_decode(p, wg, xcd, &tm.group, &tm.member)) return false;
   tm.lane = threadIdx.x & 63;
   tm.w = threadIdx.x >> 6;
   tm.team = tm.w / (KS + 1);
@@ -129,6 +128,26 @@ __device__ __forceinline__ bool team_setup(const Plan& p, Team& tm, uint32_t* cl
   tm.slab = tm.group % p.nslab;
   tm.dt = tm.member * p.NDT + tm.team;
   tm.wgi = tm.group * p.wpg + tm.member;
+  return true;
+}
+
+// A scout claims the next scout slot of its XCD (counters after the members')
+// and takes the group of that slot; a slot beyond the XCD's groups leaves.
+__device__ __forceinline__ bool scout_setup(const Plan& p, Team& tm, uint32_t* claim, float* lds) {
+  volatile uint32_t* s_slot = reinterpret_cast<volatile uint32_t*>(lds);
+  const int xcd = (int)(xcc_id() & 15u);
+  if (threadIdx.x == 0)
+    *s_slot = xcd < kXcds ? __hip_atomic_fetch_add(claim + ((long)p.ngroups + p.g0) * kXcds + xcd, 1u,
+                                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                          : 0xffffffffu;
+  __syncthreads();
+  const uint32_t slot = *s_slot;
+  __syncthreads();
+  const int local = (int)slot * kXcds + xcd;
+  if (slot >= (uint32_t)((p.gcount + kXcds - 1) / kXcds) || local >= p.gcount) return false;
+  tm.group = p.g0 + local;
+  tm.n = tm.group / p.nslab;
+  tm.slab = tm.group % p.nslab;
   return true;
 }
 
@@ -559,6 +578,54 @@ __device__ void fwd_io(const FwdArgs& a, const Team& tm, float* xring, float* os
   if (a.prof) prof.flush_trace(a.prof + 256, tm);
 }
 
+constexpr int kScoutLead = 6;  // step (iteration) a scout touches when step j is published: j + kScoutLead
+constexpr uint32_t kScoutPatience = 1u << 12;  // polls a scout waits for one step
+// Scout of a group, forward: touches the Wx lines of the group's real batch
+// rows a few steps before the I/O waves load them (see bwd_scout), paced by
+// the hidden-state word member 0 publishes each step.
+template <int CELL, int MMA>
+__device__ void fwd_scout(const FwdArgs& a, const Team& tm, float* lds) {
+  constexpr int GW = CellShape<CELL>::GW;
+  const Plan& p = a.p;
+  const int T = p.T, N = p.N, D = p.D, B = p.B;
+  const int esz = p.dt_io == DT_F32 ? 4 : 2;
+  const int b0 = tm.slab * p.BS, nreal = min(p.BS, B - b0);
+  const int row_bytes = D * esz, lpr = (row_bytes + 127) / 128 + 1;  // lines of one row (+1: unaligned rows)
+  const int nt = nreal * GW * lpr;
+  auto lptr = (__attribute__((address_space(3))) void*)(lds + (threadIdx.x >> 6) * 64);
+  auto touch = [&](int u) {
+    for (int i = threadIdx.x; i < nt; i += blockDim.x) {
+      const int r = i / (GW * lpr), g = (i / lpr) % GW, l = i % lpr;
+      const long e0 = ((((long)(b0 + r) * p.Ttot + p.t0 + u) * GW + g) * N + tm.n) * D;
+      __builtin_amdgcn_global_load_lds(static_cast<const char*>(a.wx) + e0 * esz + min(128 * l, row_bytes - 4), lptr,
+                                       4, 0, 0);
+    }
+  };
+  const char* xw = a.xbuf + (long)tm.group * p.BS * D * (MMA == MMA_F32 ? 8 : 4);
+  const long xpar_b = (long)p.ngroups * p.BS * D * (MMA == MMA_F32 ? 8 : 4);
+  auto published = [&](int t) {
+    const uint32_t w = __hip_atomic_load(reinterpret_cast<const uint32_t*>(xw + (t & 1) * xpar_b) + (MMA == MMA_F32 ? 1 : 0),
+                                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return (MMA == MMA_F32 ? w : (w >> 16)) == step_tag(t);
+  };
+  for (int u = 3; u < kScoutLead && u < T; ++u) touch(u);
+  // patience per step: a scout that loses the pace gives up within ~1 ms
+  const uint32_t patience = a.spin_limit < kScoutPatience ? a.spin_limit : kScoutPatience;
+  bool live = true;
+  for (int j = 0; live && j + kScoutLead < T; ++j) {
+    uint32_t spins = 0;
+    while (!published(j)) {
+      __builtin_amdgcn_s_sleep(2);
+      if (++spins >= patience || ((spins & 255u) == 0 && load_status(a.status) != 0)) {
+        live = false;
+        break;
+      }
+    }
+    if (live) touch(j + kScoutLead);
+  }
+  __builtin_amdgcn_s_waitcnt(0);
+}
+
 template <int CELL, int MMA, int KTW, int NB, int NDT, int KSC>
 __global__ void __launch_bounds__(64 * (KSC + 1) * NDT) fwd_kernel(FwdArgs a) {
   using CS = CellShape<CELL>;
@@ -568,6 +635,10 @@ __global__ void __launch_bounds__(64 * (KSC + 1) * NDT) fwd_kernel(FwdArgs a) {
   const Plan& p = a.p;
   extern __shared__ float lds[];
   Team tm;
+  if (blockIdx.x >= p.grid - scout_blocks(p)) {  // a scout
+    if (scout_setup(p, tm, a.claim, lds)) fwd_scout<CELL, MMA>(a, tm, lds);
+    return;
+  }
   if (!team_setup(p, tm, a.claim, a.status, KSC, lds)) return;
   const int D = p.D, B = p.B, T = p.T, N = p.N;
 
@@ -908,7 +979,6 @@ __device__ void bwd_io(const BwdArgs& a, const Team& tm, float* iring, float* os
 // never read). The scout paces itself by the exchange word that member 0
 // publishes each iteration; nothing waits for it, and every wait of its own is
 // bounded (spin limit, sticky status), so it always finishes.
-constexpr int kScoutLead = 6;  // iteration the scout touches when iteration j is published: j + kScoutLead
 template <int CELL, int MMA>
 __device__ void bwd_scout(const BwdArgs& a, const Team& tm, float* lds) {
   using CS = CellShape<CELL>;
@@ -953,12 +1023,14 @@ __device__ void bwd_scout(const BwdArgs& a, const Team& tm, float* lds) {
   };
   // Every wave paces itself (a barrier-paced variant measured slower).
   for (int x = 3; x < kScoutLead && x < T; ++x) touch(x);
-  uint32_t spins = 0;
+  // patience per step: a scout that loses the pace gives up within ~1 ms
+  const uint32_t patience = a.spin_limit < kScoutPatience ? a.spin_limit : kScoutPatience;
   bool live = true;
   for (int j = 0; live && j + kScoutLead < T; ++j) {
+    uint32_t spins = 0;
     while (!published(j)) {
       __builtin_amdgcn_s_sleep(2);
-      if (++spins >= a.spin_limit || ((spins & 255u) == 0 && load_status(a.status) != 0)) {
+      if (++spins >= patience || ((spins & 255u) == 0 && load_status(a.status) != 0)) {
         live = false;
         break;
       }
@@ -979,11 +1051,11 @@ __global__ void __launch_bounds__(64 * (KSC + 1) * NDT) bwd_kernel(BwdArgs a) {
   const Plan& p = a.p;
   extern __shared__ float lds[];
   Team tm;
-  if (!team_setup<true>(p, tm, a.claim, a.status, KSC, lds)) return;
-  if (tm.member == p.wpg) {  // the group's scout
-    bwd_scout<CELL, MMA>(a, tm, lds);
+  if (blockIdx.x >= p.grid - scout_blocks(p)) {  // a scout
+    if (scout_setup(p, tm, a.claim, lds)) bwd_scout<CELL, MMA>(a, tm, lds);
     return;
   }
+  if (!team_setup(p, tm, a.claim, a.status, KSC, lds)) return;
   const int D = p.D, B = p.B, N = p.N, T = p.T;
   const int GD = GR * D;
   const bool cut = (p.flags & kFlagCut) != 0;
