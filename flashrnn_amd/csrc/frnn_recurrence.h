@@ -237,6 +237,12 @@ struct Prof {
 };
 
 
+// Work a gather runs once, right after it issues its first poll's loads (the
+// wait for them then overlaps it).
+struct NoWork {
+  __device__ __forceinline__ void operator()() const {}
+};
+
 // Runs a wave keeps in flight at most (8 BF16 runs or 4 FP32 runs: 64
 // registers; 4 runs in two-tile workgroups, whose resident slice is larger);
 // a longer contraction range is polled chunk by chunk, which bounds the
@@ -256,10 +262,12 @@ template <int MMA, int NDT> struct PollChunk {
 // Ranges of more than PollChunk runs are polled in chunks: each chunk is
 // polled until all of its tags are fresh and only then multiplied, so a
 // stale chunk never has to be taken back out of the accumulators.
-template <int MMA, int NDT, int NB, int NF, bool SPLIT = false, bool SPEC = true, typename Zero, typename Prod>
+template <int MMA, int NDT, int NB, int NF, bool SPLIT = false, bool SPEC = true, typename Zero, typename Prod,
+          typename Between = NoWork>
 __device__ __forceinline__ uint32_t gather_mma(const Xchg& x, const int (&word)[NB][NF], const bool (&bval)[NB],
                                                int off, int cstride, int nf, uint32_t tag, uint32_t* status, uint32_t spin_limit,
-                                               bool& abort, Zero zero, Prod prod) {
+                                               bool& abort, Zero zero, Prod prod, Between between = Between{}) {
+  bool first = true;
   using Op = Operand<MMA, SPLIT>;
   uint32_t spins = 0;
   if constexpr (NF <= PollChunk<MMA, NDT>::value && SPEC) {
@@ -274,6 +282,10 @@ __device__ __forceinline__ uint32_t gather_mma(const Xchg& x, const int (&word)[
           r[bt][j].zero();
           if (j < nf && bval[bt]) xload<MMA>(x, word[bt][j] + off, cstride, r[bt][j]);
         }
+      if (first) {
+        between();
+        first = false;
+      }
       // Branch-free from here on: the MFMAs read operands across lanes and must
       // run with the whole wave active, so lane-dependent conditions are selects.
       bool ok = true;
@@ -313,6 +325,10 @@ __device__ __forceinline__ uint32_t gather_mma(const Xchg& x, const int (&word)[
             r[bt][jj].zero();
             if (c0 + jj < NF && c0 + jj < nf && bval[bt]) xload<MMA>(x, word[bt][c0 + jj < NF ? c0 + jj : 0] + off, cstride, r[bt][jj]);
           }
+        if (first) {
+          between();
+          first = false;
+        }
         bool ok = true;
 #pragma unroll
         for (int bt = 0; bt < NB; ++bt)
@@ -351,10 +367,12 @@ __device__ __forceinline__ uint32_t gather_mma(const Xchg& x, const int (&word)[
 // half the loads; the odd tile then moves down 8 lanes (DPP) and the upper
 // lanes contribute zero. word[j] is the run of k-tile j for batch row lane % 8.
 // Long ranges are polled in chunks of PollChunk pairs, as in gather_mma.
-template <int MMA, int NDT, int NF, bool SPLIT = false, bool SPEC = true, typename Zero, typename Prod>
+template <int MMA, int NDT, int NF, bool SPLIT = false, bool SPEC = true, typename Zero, typename Prod,
+          typename Between = NoWork>
 __device__ __forceinline__ uint32_t gather_pair_mma(const Xchg& x, const int (&word)[NF], bool bv, int off, int cstride, int nf,
                                                     uint32_t tag, uint32_t* status, uint32_t spin_limit, bool& abort,
-                                                    Zero zero, Prod prod) {
+                                                    Zero zero, Prod prod, Between between = Between{}) {
+  bool first = true;
   using Op = Operand<MMA, SPLIT>;
   constexpr int NP = (NF + 1) / 2;
   constexpr int CH = NP <= PollChunk<MMA, NDT>::value ? NP : PollChunk<MMA, NDT>::value;
@@ -387,6 +405,10 @@ __device__ __forceinline__ uint32_t gather_pair_mma(const Xchg& x, const int (&w
         const int i = i0 + ii;
         r[ii].zero();
         if (i < NP && 2 * i + hi < nf && bv) xload<MMA>(x, word[i < NP ? 2 * i + hi : 0] + off, cstride, r[ii]);
+      }
+      if (first) {
+        between();
+        first = false;
       }
       // Branch-free from here on (cross-lane DPP and MFMA need the whole wave).
       bool ok = true;
@@ -753,7 +775,23 @@ __global__ void __launch_bounds__(64 * (KSC + 1) * NDT) fwd_kernel(FwdArgs a) {
 #pragma unroll
       for (int g = 0; g < GW; ++g) xnext[s][g] = xr[xw[s][g]];
   };
-  read_x(0);
+  // The owners stage step t-1's outputs for the I/O wave and read step t's Wx
+  // from the ring while step t's first poll is in flight (gather's `between`):
+  // the poll goes out right after the loop head. The staging area of step t-1
+  // is drained after barrier t, its ring slot was filled before barrier t-1.
+  float sv_keep[EPLMAX][NSAVE];
+  auto stage = [&](int t) {
+    float* os = ost + (long)(t & 1) * NV * NE;
+#pragma unroll
+    for (int s = 0; s < EPLMAX; ++s) {
+      if (!own[s]) continue;
+      const int e = oe[s];
+#pragma unroll
+      for (int k = 0; k < S; ++k) os[k * NE + e] = st[s][k];
+#pragma unroll
+      for (int v = 0; v < NSAVE; ++v) os[(S + v) * NE + e] = sv_keep[s][v];
+    }
+  };
   bool abort = false;
   for (int t = 0; t < T; ++t) {
     prof.stamp(t, 0);
@@ -769,15 +807,19 @@ __global__ void __launch_bounds__(64 * (KSC + 1) * NDT) fwd_kernel(FwdArgs a) {
 #pragma unroll
       for (int g = 0; g < GR; ++g) acc[bt][g] = mma(A[g][j], f, acc[bt][g]);
     };
+    auto between = [&]() {
+      if (t >= 1) stage(t - 1);
+      read_x(t);
+    };
     {
       uint32_t polls;
       const int off = ((t - 1) & 1) * xpar;
       if (NB == 1 && pair)
         polls = gather_pair_mma<MMA, NDT, KTW>(xc, xword_pair, bv_pair, off, cstride, nkt, ptag(p, t - 1), a.status,
-                                               a.spin_limit, abort, zero, prod);
+                                               a.spin_limit, abort, zero, prod, between);
       else
         polls = gather_mma<MMA, NDT, NB, KTW>(xc, xword, bval, off, cstride, nkt, ptag(p, t - 1), a.status,
-                                              a.spin_limit, abort, zero, prod);
+                                              a.spin_limit, abort, zero, prod, between);
       prof.add(4, polls);
     }
     prof.mark(0);
@@ -797,8 +839,7 @@ __global__ void __launch_bounds__(64 * (KSC + 1) * NDT) fwd_kernel(FwdArgs a) {
     prof.mark(2);
     prof.stamp(t, 2);
 
-    // ---- 3. owners: gates, cell, staged outputs, exchange
-    float* os = ost + (long)(t & 1) * NV * NE;
+    // ---- 3. owners: gates, cell, exchange (the outputs are staged during the next poll)
 #pragma unroll
     for (int s = 0; s < EPLMAX; ++s) {
       if (!own[s]) continue;
@@ -835,14 +876,12 @@ __global__ void __launch_bounds__(64 * (KSC + 1) * NDT) fwd_kernel(FwdArgs a) {
         xstore<MMA>(xc, (t & 1) * xpar + xgrp + xword_of<MMA>(p.BS, el[s].bl, el[s].d), st[s][0], step_tag(t));
       if (s == 0) prof.stamp(t, 3);
 #pragma unroll
-      for (int k = 0; k < S; ++k) os[k * NE + e] = st[s][k];
-#pragma unroll
-      for (int v = 0; v < NSAVE; ++v) os[(S + v) * NE + e] = sv[v];
+      for (int v = 0; v < NSAVE; ++v) sv_keep[s][v] = sv[v];
     }
-    if (t + 1 < T) read_x(t + 1);  // landed before barrier t
     prof.mark(3);
     prof.stamp(t, 4);
   }
+  stage(T - 1);
   lds_barrier();  // the I/O wave drains the last step
 
   // ---- carry: the last state in full precision
