@@ -30,9 +30,9 @@
 
 namespace frnn {
 
-constexpr int kFwdRing = 4;   // Wx ring slots in LDS
-constexpr int kFwdAhead = 3;  // steps of Wx in flight: one less than the slots, so a
-                              // load never lands in the slot the owners are reading
+constexpr int kFwdRing = 2;   // raw Wx slots in LDS (DMA targets)
+constexpr int kFwdXf = 3;     // converted (FP32) Wx slots in LDS (what the owners read)
+constexpr int kFwdAhead = 3;  // steps a Wx load goes out ahead of its use
 
 template <int CELL>
 struct BwdRing {  // input steps staged ahead, bounded by the I/O wave's registers
@@ -49,6 +49,8 @@ struct BwdRing {  // input steps staged ahead, bounded by the I/O wave's registe
 //                   4*quad..+7 in the even quads, odd quads unused)
 //             ost  [2][value][NE]                         states + saved values,
 //                  value-major so the drain reads 4 elements per 16-byte read
+//             xf   [slot][gate][NE]                       Wx of a step in FP32,
+//                  converted from the raw slot by the I/O wave
 //   backward: red  [2][NB][KS][304]                       partial R^T dG at
 //                  red_idx(lane*4 + reg): 16 spare floats per 64, so the
 //                  16-byte writes and the owners' scalar reads are conflict-free
@@ -66,8 +68,9 @@ struct Lds {
   static constexpr int RING = GW * 64 * 4;                   // floats per Wx ring slot
   static constexpr int RED_F = 272 * 4;  // floats per (wave, batch tile), forward partials
   static constexpr int RED_B = 304;      // floats per (batch tile, wave), backward partials
+  static constexpr int XF = GW * NE;                         // floats per converted Wx slot
   __host__ __device__ static constexpr long fwd(int KS) {
-    return 2L * KS * NB * RED_F + (long)kFwdRing * RING + 2L * NV * NE;
+    return 2L * KS * NB * RED_F + (long)kFwdRing * RING + 2L * NV * NE + (long)kFwdXf * XF;
   }
   __host__ __device__ static constexpr long bwd(int KS) {
     return 2L * NB * KS * RED_B + (long)BwdRing<CELL>::P * NE * NOP + 2L * NE * NOB;
@@ -475,33 +478,16 @@ __device__ __forceinline__ void wait_vm() {
   __builtin_amdgcn_s_waitcnt((n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
-// Wx of gate g for owned element (slab row r, unit d of the tile) in a raw
-// ring slot (see the LDS layout above): the 32-bit word that holds it, read
-// raw so the owners issue every gate's read at once and convert only at the
-// next step's cell, and the value from that word.
-__device__ __forceinline__ int ring_word(int g, int r, int d, int dt) {
-  return dt == DT_F32 ? (g * 64 + r * 4 + (d >> 2)) * 4 + (d & 3) : (g * 64 + r * 4 + (d >> 3) * 2) * 4 + ((d & 7) >> 1);
-}
-// Branch-free in the runtime dtype: every form is computed and one selected.
-__device__ __forceinline__ float ring_val(uint32_t w, int d, int dt) {
-  const uint32_t h = (w >> ((d & 1) * 16)) & 0xffffu;
-  const float vf = u2f(w), vb = u2f(h << 16), vh = f16_to_f32(h);
-  const float v16 = dt == DT_F16 ? vh : vb;
-  return dt == DT_F32 ? vf : v16;
-}
-
-// I/O wave of a team. Wx of step u is loaded straight into ring slot
-// u % kFwdRing by LDS-DMA (global_load_lds: no registers in flight), issued
-// kFwdAhead steps ahead; before barrier t the wave waits, by count, until the
-// loads of step t+1 have landed, so the owners read step t+1's Wx right after
-// their step-t cell, off the critical path. It then issues the loads of step
-// t+kFwdAhead and, after barrier t, drains the outputs of step t-1. Per step
-// the wave issues the same loads and stores in the same order, so the count of
-// operations issued after a step's loads is a constant in the steady state
-// (the first and last steps wait for everything). Padding batch rows are
-// neither loaded nor stored.
+// I/O wave of a team. Wx of step u is loaded straight into raw slot u % 2 by
+// LDS-DMA (global_load_lds: no registers in flight), three steps ahead; two
+// steps ahead of its use the wave converts it to FP32 in slot u % 3 of the
+// area the owners read (so the runtime dtype is off their critical path). After barrier t it also drains step t-1's
+// outputs from the staging area. Per step the wave issues the same loads and
+// stores in the same order, so the count of operations issued after a step's
+// loads is a constant in the steady state. Padding batch rows are neither
+// loaded nor stored (their converted values are never used).
 template <int CELL, int MMA, int NB>
-__device__ void fwd_io(const FwdArgs& a, const Team& tm, float* xring, float* ost) {
+__device__ void fwd_io(const FwdArgs& a, const Team& tm, float* xring, float* ost, float* xf) {
   static_assert(NB == 1, "one 16-row batch tile per group");
   using CS = CellShape<CELL>;
   constexpr int GW = CS::GW, S = CS::S, NE = NB * 256, P = kFwdAhead;
@@ -549,45 +535,65 @@ __device__ void fwd_io(const FwdArgs& a, const Team& tm, float* xring, float* os
         *reinterpret_cast<f32x4*>(a.save + save_index(p, NE, t, tm.wgi, v - S, tm.team, e0)) = x;
     }
   };
-  // Per iteration t: wait for the loads of step t+1; barrier t; issue the
-  // loads of step t+P; drain step t-1. The HBM loads go out first, as early as
-  // the ring allows: the CU's vector-memory path returns data in order, so
-  // loads issued later would hold up the compute waves' exchange polls behind
-  // their HBM latency. VMEM operations issued after the loads of step t+1, at
-  // the top of iteration t (steady state, t >= P): the stores of the iteration
-  // that issued them, then P-2 iterations of loads and stores.
-  static_assert(P >= 2, "prefetch distance");
+
+  // Conversion of a landed raw slot into FP32 for the owners: lane l converts
+  // four units of one row (the elements e0 .. e0+3 it also stores), one 8- or
+  // 16-byte LDS read and one 16-byte write per gate. (The owners still add the
+  // bias after Ry, in the reference's order: (x + Ry) + b and x + (b + Ry)
+  // round differently, and a sLSTM max or clamp can break the other way.)
+  auto convert = [&](int u) {
+    const float* slot = xring + (long)(u % kFwdRing) * RING;
+    float* dst = xf + (long)(u % kFwdXf) * Lds<CELL, NB>::XF;
+#pragma unroll
+    for (int g = 0; g < GW; ++g) {
+      f32x4 x;
+      if (p.dt_io == DT_F32) {
+        x = *reinterpret_cast<const f32x4*>(slot + g * 256 + (lrow * 4 + lquad) * 4);
+      } else {
+        const uint2 h = *reinterpret_cast<const uint2*>(reinterpret_cast<const char*>(slot + g * 256) +
+                                                        (lrow * 4 + (lquad >> 1) * 2) * 16 + (lquad & 1) * 8);
+        x = raw4_f32(u32x4{h.x, h.y, 0u, 0u}, p.dt_io);
+      }
+      *reinterpret_cast<f32x4*>(dst + g * NE + e0) = x;
+    }
+  };
+  // Per iteration t: barrier t; convert step t+2 (its loads went out in
+  // iteration t-1; the owners read it after barrier t+1); issue the loads of
+  // step t+P; drain step t-1. The loads go out right after the barrier: the
+  // CU's vector memory returns data in issue order, so loads issued later would
+  // hold up the compute waves' exchange polls behind them. VMEM operations
+  // issued after the loads of step t+2 (t >= 2): the stores of iteration t-1.
+  static_assert(P == 3, "the conversion waits assume the loads of step t+2 go out in iteration t-1");
   // stores per step: the policy's states (S, 1 or none in the loop) plus the saves when training
   constexpr int kStTrain = NV, kStTrainHidden = 1 + NSAVE, kStFull = S, kStHidden = 1;
-  constexpr int kAfterTrain = kStTrain + (P - 2) * (GW + kStTrain);
-  constexpr int kAfterTrainHidden = kStTrainHidden + (P - 2) * (GW + kStTrainHidden);
-  constexpr int kAfterFull = kStFull + (P - 2) * (GW + kStFull);
-  constexpr int kAfterHidden = kStHidden + (P - 2) * (GW + kStHidden), kAfterLast = (P - 2) * GW;
 
   Prof prof;
   prof.init(a.prof != nullptr && blockIdx.x == 0, a.prof != nullptr);
-  for (int u = 0; u < P && u < T; ++u) load_wx(u);
+  for (int u = 0; u < 2 && u < T; ++u) load_wx(u);
   wait_vm<0>();
-  lds_barrier();  // Wx_0 in its slot
+  for (int u = 0; u < 2 && u < T; ++u) convert(u);
+  lds_barrier();  // Wx of steps 0 and 1 converted; both raw slots read
+  if (2 < T) load_wx(2);
   for (int t = 0; t < T; ++t) {
-    if (t >= P && t + P <= T) {
-      if (training && mode == 0) wait_vm<kAfterTrain>();
-      else if (training) wait_vm<kAfterTrainHidden>();
-      else if (mode == 0) wait_vm<kAfterFull>();
-      else if (mode == 1) wait_vm<kAfterHidden>();
-      else wait_vm<kAfterLast>();
-    } else {
-      wait_vm<0>();
-    }
     prof.mark(0);
     prof.stamp(t, 0);
-    prof.mark(1);
-    prof.stamp(t, 1);
-    lds_barrier();  // step t: Wx_{t+1} in its slot; outputs of step t-1 staged
+    lds_barrier();  // step t: outputs of step t-1 staged
     prof.mark(2);
     prof.stamp(t, 2);
-    // slot (t+P) % kFwdRing held step t-1, which every owner finished reading
-    // before barrier t-1
+    if (t + 2 < T) {
+      if (t <= 1) wait_vm<0>();
+      else {
+        if (training && mode == 0) wait_vm<kStTrain>();
+        else if (training) wait_vm<kStTrainHidden>();
+        else if (mode == 0) wait_vm<kStFull>();
+        else if (mode == 1) wait_vm<kStHidden>();
+        else wait_vm<0>();
+      }
+      convert(t + 2);
+    }
+    prof.mark(1);
+    prof.stamp(t, 1);
+    // raw slot (t+3) % 2 held step t+1, converted before barrier t
     if (t + P < T) load_wx(t + P);
     if (t >= 1) store_out(t - 1, ost + ((t - 1) & 1) * NV * NE);
     prof.mark(3);
@@ -668,6 +674,7 @@ __global__ void __launch_bounds__(64 * (KSC + 1) * NDT) fwd_kernel(FwdArgs a) {
   float* red = lds + tm.team * Lds<CELL, NB>::fwd(KS);  // [2][KS][NB][272][4]
   float* xring = red + 2L * KS * NB * RED_F;            // [slot][gate][64][4]
   float* ost = xring + (long)kFwdRing * RING;           // [2][NV][NE]
+  float* xf = ost + 2L * NV * NE;                       // [slot][gate][NE]
 
   // sLSTM: the reference's global predicate all(n0 == 0) over the call's whole initial state,
   // at the first step of a sequence only (a later window continues from a carry)
@@ -681,7 +688,7 @@ __global__ void __launch_bounds__(64 * (KSC + 1) * NDT) fwd_kernel(FwdArgs a) {
     }
   }
   if (tm.kw == KS) {
-    fwd_io<CELL, MMA, NB>(a, tm, xring, ost);
+    fwd_io<CELL, MMA, NB>(a, tm, xring, ost, xf);
     return;
   }
 
@@ -761,19 +768,15 @@ __global__ void __launch_bounds__(64 * (KSC + 1) * NDT) fwd_kernel(FwdArgs a) {
   __builtin_amdgcn_s_waitcnt(0);
   lds_barrier();  // Wx_0 in its slot
   // Wx of the next step, read from the ring right after each cell
-  // (raw words: the reads are waited for at the next barrier, not here)
-  uint32_t xnext[EPLMAX][GW];
-  int xw[EPLMAX][GW];
-#pragma unroll
-  for (int s = 0; s < EPLMAX; ++s)
-#pragma unroll
-    for (int g = 0; g < GW; ++g) xw[s][g] = ring_word(g, el[s].bl & 15, el[s].d & 15, p.dt_io);
+  // Wx of the step, FP32, converted by the I/O wave (the reads are waited for
+  // at the barrier, not here)
+  float xnext[EPLMAX][GW];
   auto read_x = [&](int u) {
-    const uint32_t* xr = reinterpret_cast<const uint32_t*>(xring + (long)(u % kFwdRing) * RING);
+    const float* xr = xf + (long)(u % kFwdXf) * Lds<CELL, NB>::XF;
 #pragma unroll
     for (int s = 0; s < EPLMAX; ++s)
 #pragma unroll
-      for (int g = 0; g < GW; ++g) xnext[s][g] = xr[xw[s][g]];
+      for (int g = 0; g < GW; ++g) xnext[s][g] = xr[g * NE + (oe[s] & (NE - 1))];
   };
   // The owners stage step t-1's outputs for the I/O wave and read step t's Wx
   // from the ring while step t's first poll is in flight (gather's `between`):
@@ -850,13 +853,13 @@ __global__ void __launch_bounds__(64 * (KSC + 1) * NDT) fwd_kernel(FwdArgs a) {
       for (int w2 = 0; w2 < KS; ++w2) part[w2] = *reinterpret_cast<const f32x4*>(rp + w2 * NB * RED_F + src);
       float xcur[GW];
 #pragma unroll
-      for (int g = 0; g < GW; ++g) xcur[g] = el[s].real ? ring_val(xnext[s][g], el[s].d, p.dt_io) : 0.f;
+      for (int g = 0; g < GW; ++g) xcur[g] = xnext[s][g];
       float ry[GR];
 #pragma unroll
       for (int g = 0; g < GR; ++g) {
-        float v = 0.f;
+        float v = part[0][g];
 #pragma unroll
-        for (int w2 = 0; w2 < KS; ++w2) v += part[w2][g];
+        for (int w2 = 1; w2 < KS; ++w2) v += part[w2][g];
         ry[g] = v;
       }
       float sv[NSAVE];
