@@ -251,6 +251,14 @@ struct Xchg {
 
 __device__ __forceinline__ uint32_t split_word(float v, uint32_t tag) { return ((f2u(v) + 2u) & ~3u) | tag; }
 
+// The exchange region is global memory: say so to the compiler, so the stores
+// stay global ones (a flat store would also count in lgkmcnt) even when the
+// base pointer has been moved to VGPRs.
+template <typename T>
+__device__ __forceinline__ __attribute__((address_space(1))) T* gptr(T* p) {
+  return (__attribute__((address_space(1))) T*)p;
+}
+
 // Store one exchange word. Same-XCD mode uses a non-temporal store (it lands
 // in the shared L2); the placement-free mode uses an agent-scope store.
 template <int MMA, bool SPLIT = false>
@@ -259,12 +267,12 @@ __device__ __forceinline__ void xstore(const Xchg& x, long word, float v, uint32
     uint32_t w = SPLIT ? split_word(v, tag) : ((tag << 16) | op_bits<MMA>(v));
     uint32_t* p = reinterpret_cast<uint32_t*>(x.base) + word;
     if (x.shared_xcd) __hip_atomic_store(p, w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    else __builtin_nontemporal_store(w, p);
+    else __builtin_nontemporal_store(w, gptr(p));
   } else {
     uint64_t w = ((uint64_t)tag << 32) | f2u(v);
     uint64_t* p = reinterpret_cast<uint64_t*>(x.base) + word;
     if (x.shared_xcd) __hip_atomic_store(p, w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    else __builtin_nontemporal_store(w, p);
+    else __builtin_nontemporal_store(w, gptr(p));
   }
 }
 
@@ -282,7 +290,7 @@ __device__ __forceinline__ void xstore_vec(const Xchg& x, long word, const float
 #pragma unroll
       for (int i = 0; i < NV; ++i) __hip_atomic_store(p + i, w[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     } else {
-      __builtin_nontemporal_store(w, reinterpret_cast<vec_t*>(p));
+      __builtin_nontemporal_store(w, gptr(reinterpret_cast<vec_t*>(p)));
     }
   } else {
 #pragma unroll
