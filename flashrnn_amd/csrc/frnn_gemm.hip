@@ -7,6 +7,7 @@
 #include "frnn_kernels.h"
 #include "frnn_plan.h"
 
+
 namespace frnn {
 
 // ============================================================== dR GEMM
@@ -44,51 +45,43 @@ __device__ __forceinline__ void gemm_frag(const typename GemmElem<MMA>::type* ro
   }
 }
 
-// Operand runs of 8 contiguous columns for k = (b, t): dG (m = g*D + o) and h_{t-1} (q).
-struct GemmSrc {
-  const GemmArgs* a;
-  int n;
-  __device__ __forceinline__ void load(long k, int m, int q, f32x4 (&va)[2], f32x4 (&vh)[2]) const {
-    const Plan& p = a->p;
-    const long K = (long)p.B * p.T;
-    va[0] = va[1] = vh[0] = vh[1] = f32x4{0.f, 0.f, 0.f, 0.f};
-    if (k >= K) return;
-    const long b = k / p.T, t = k % p.T;
-    const int g = m / p.D, o = m % p.D;
-    if (p.cell == CELL_GRU && g == 0) {
-      const float* src = a->dcand + ((b * p.T + t) * p.N + n) * p.D + o;
-      va[0] = *reinterpret_cast<const f32x4*>(src);
-      va[1] = *reinterpret_cast<const f32x4*>(src + 4);
-    } else {
-      const int gw = p.cell == CELL_GRU ? g - 1 : g;
-      const long i = (b * p.T + t) * p.GW * p.N * p.D + ((long)gw * p.N + n) * p.D + o;
-      va[0] = ld4(a->dwx, i, p.dt_io);
-      va[1] = ld4(a->dwx, i + 4, p.dt_io);
-    }
-    if (t == 0) {
-      const long i = (b * p.N + n) * p.D + q;  // h_{-1} = s0[0]
-      vh[0] = ld4(a->s0, i, p.dt_state);
-      vh[1] = ld4(a->s0, i + 4, p.dt_state);
-    } else {
-      const long i = ((b * p.T + t - 1) * p.N + n) * p.D + q;  // h_{t-1} = states[0][b][t-1]
-      vh[0] = ld4(a->states, i, p.dt_out);
-      vh[1] = ld4(a->states, i + 4, p.dt_out);
-    }
-  }
+// Operand runs of 8 contiguous columns for k = (b, t): dG (m = g*D + o) and
+// h_{t-1} (q). A run's column offset is fixed for the whole kernel and its k
+// advances by a constant per stage, so the (b, t) of a run is carried from
+// stage to stage instead of being divided out of k each time.
+struct GemmRunA {  // dG run: columns m .. m+7 of k = (b, t)
+  const void* base;  // dwx (or the GRU candidate buffer) at this run's column, k = 0
+  bool f32;          // the candidate buffer (FP32), else dwx in dt_io
+  long kstride;      // elements between consecutive t
+  int b, t;
 };
+struct GemmRunH {  // h_{t-1} run: columns q .. q+7
+  int b, t;
+};
+
+__device__ __forceinline__ void gemm_advance(int& b, int& t, int dk, int T) {
+  t += dk;
+  while (t >= T) {
+    t -= T;
+    ++b;
+  }
+}
 
 // Workgroup tile (32*WM) x (32*WQ) of part[split][n][m][q], WM*WQ waves of 32x32
 // each; k in steps of 32 through double-buffered LDS, the next step's global
 // loads in flight while the current step runs on MFMA. Operands are written to
 // LDS transposed ([column][k]) so each MFMA fragment is one 16-byte (bf16) or
 // two 16-byte (f32) reads of 8 consecutive k.
-template <int MMA, int WM, int WQ>
+// KSUB: 32-wide k sub-steps per stage (2 and 3 measured no faster than 1 at
+// the LSTM B8 T1024 N3 D256 shape).
+template <int MMA, int WM, int WQ, int KSUB>
 __global__ void __launch_bounds__(64 * WM * WQ) dr_gemm_kernel(GemmArgs a) {
   typedef typename GemmElem<MMA>::type E;
-  constexpr int LD = 40;                 // LDS row stride (32 k + pad), elements
+  constexpr int KW = 32 * KSUB;          // k per stage
+  constexpr int LD = KW + 8;             // LDS row stride (KW k + pad), elements
   constexpr int NT = 64 * WM * WQ;       // threads
-  constexpr int RA = 32 * WM * 4 / NT;   // runs of 8 per thread per step: A (32 k x 32*WM m / 8)
-  constexpr int RH = 32 * WQ * 4 / NT;   // and h
+  constexpr int RA = KW * WM * 4 / NT;   // runs of 8 per thread per stage: A (KW k x 32*WM m / 8)
+  constexpr int RH = KW * WQ * 4 / NT;   // and h
   __shared__ __attribute__((aligned(16))) E As[2][32 * WM * LD];
   __shared__ __attribute__((aligned(16))) E Hs[2][32 * WQ * LD];
   const Plan& p = a.p;
@@ -96,17 +89,21 @@ __global__ void __launch_bounds__(64 * WM * WQ) dr_gemm_kernel(GemmArgs a) {
   const int GD = p.GR * p.D;
   const int mt = GD / (32 * WM), qt = p.D / (32 * WQ);
   const int tiles = p.N * mt * qt;
-  const int split = blockIdx.x / tiles;
-  int rem = blockIdx.x % tiles;
+  // XCD-major tile order: workgroup b runs on XCD b % 8, so consecutive tiles
+  // (the m-tiles of one h block, then the q-tiles of one dG block) go to one
+  // XCD and share its L2 instead of being fetched once per XCD.
+  const int full = (int)(gridDim.x / kXcds) * kXcds, bx = blockIdx.x;
+  const int tile_id = bx < full ? (bx % kXcds) * (full / kXcds) + bx / kXcds : bx;
+  const int split = tile_id / tiles;
+  int rem = tile_id % tiles;
   const int n = rem / (mt * qt);
   rem %= mt * qt;
-  const int m0 = (rem / qt) * 32 * WM, q0 = (rem % qt) * 32 * WQ;
+  const int m0 = (rem % mt) * 32 * WM, q0 = (rem / mt) * 32 * WQ;  // m-tiles of one q block adjacent
   const long K = (long)p.B * p.T;
-  const long KT = (K + 31) / 32;
+  const long KT = (K + KW - 1) / KW;
   const long s_lo = KT * split / p.splitk, s_hi = KT * (split + 1) / p.splitk;
   const int row = lane & 15, kq = lane >> 4;
   const int wm = w % WM, wq = w / WM;
-  GemmSrc src{&a, n};
 
   f32x4 acc[2][2];
 #pragma unroll
@@ -115,19 +112,71 @@ __global__ void __launch_bounds__(64 * WM * WQ) dr_gemm_kernel(GemmArgs a) {
     for (int j = 0; j < 2; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   // per-thread runs: A run c -> (k = c / (4*WM), column 8*(c % (4*WM))), h likewise with WQ
+  const long K0 = (long)KW * s_lo;
+  const long wxt = (long)p.GW * p.N * p.D;  // dwx elements per (b, t)
+  GemmRunA ga[RA];
+  GemmRunH gh[RH];
+#pragma unroll
+  for (int r = 0; r < RA; ++r) {
+    const int c = tid + NT * r, m = m0 + 8 * (c % (4 * WM));
+    const long k = K0 + c / (4 * WM);
+    ga[r].b = (int)(k / p.T);
+    ga[r].t = (int)(k % p.T);
+    const int g = m / p.D, o = m % p.D;
+    if (p.cell == CELL_GRU && g == 0) {
+      ga[r].base = a.dcand + (long)n * p.D + o;
+      ga[r].f32 = true;
+      ga[r].kstride = (long)p.N * p.D;
+    } else {
+      const int gw = p.cell == CELL_GRU ? g - 1 : g;
+      ga[r].base = static_cast<const char*>(a.dwx) + (((long)gw * p.N + n) * p.D + o) * (p.dt_io == DT_F32 ? 4 : 2);
+      ga[r].f32 = false;
+      ga[r].kstride = wxt;
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < RH; ++r) {
+    const int c = tid + NT * r;
+    const long k = K0 + c / (4 * WQ);
+    gh[r].b = (int)(k / p.T);
+    gh[r].t = (int)(k % p.T);
+  }
   f32x4 ra[RA][2], rh[RH][2];
-  auto fetch = [&](long s) {
+  auto fetch = [&]() {  // the runs' current (b, t); then advance them one stage
 #pragma unroll
     for (int r = 0; r < RA; ++r) {
-      const int c = tid + NT * r;
-      f32x4 dummy[2];
-      src.load(32 * s + c / (4 * WM), m0 + 8 * (c % (4 * WM)), q0, ra[r], dummy);
+      const int c = tid + NT * r, b = ga[r].b, t = ga[r].t;
+      ra[r][0] = ra[r][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+      if (b < p.B) {
+        const long i = ((long)b * p.T + t) * ga[r].kstride;
+        if (ga[r].f32) {
+          const float* src = static_cast<const float*>(ga[r].base) + i;
+          ra[r][0] = *reinterpret_cast<const f32x4*>(src);
+          ra[r][1] = *reinterpret_cast<const f32x4*>(src + 4);
+        } else {
+          ra[r][0] = ld4(ga[r].base, i, p.dt_io);
+          ra[r][1] = ld4(ga[r].base, i + 4, p.dt_io);
+        }
+      }
+      gemm_advance(ga[r].b, ga[r].t, KW, p.T);
+      (void)c;
     }
 #pragma unroll
     for (int r = 0; r < RH; ++r) {
-      const int c = tid + NT * r;
-      f32x4 dummy[2];
-      src.load(32 * s + c / (4 * WQ), m0, q0 + 8 * (c % (4 * WQ)), dummy, rh[r]);
+      const int c = tid + NT * r, q = q0 + 8 * (c % (4 * WQ)), b = gh[r].b, t = gh[r].t;
+      rh[r][0] = rh[r][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+      if (b < p.B) {
+        if (t == 0) {
+          const long i = ((long)b * p.N + n) * p.D + q;  // h_{-1} = s0[0]
+          rh[r][0] = ld4(a.s0, i, p.dt_state);
+          rh[r][1] = ld4(a.s0, i + 4, p.dt_state);
+        } else {
+          const long i = (((long)b * p.T + t - 1) * p.N + n) * p.D + q;  // h_{t-1} = states[0][b][t-1]
+          rh[r][0] = ld4(a.states, i, p.dt_out);
+          rh[r][1] = ld4(a.states, i + 4, p.dt_out);
+        }
+      }
+      gemm_advance(gh[r].b, gh[r].t, KW, p.T);
     }
   };
   auto stage = [&](int buf) {
@@ -146,23 +195,26 @@ __global__ void __launch_bounds__(64 * WM * WQ) dr_gemm_kernel(GemmArgs a) {
   };
 
   if (s_lo < s_hi) {
-    fetch(s_lo);
+    fetch();
     stage(0);
     __syncthreads();
   }
   for (long s = s_lo; s < s_hi; ++s) {
     const int buf = (int)((s - s_lo) & 1);
-    if (s + 1 < s_hi) fetch(s + 1);
-    Frag<MMA> fa[2], fh[2];
+    if (s + 1 < s_hi) fetch();
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      gemm_frag<MMA>(As[buf] + (wm * 32 + i * 16 + row) * LD + 8 * kq, fa[i]);
-      gemm_frag<MMA>(Hs[buf] + (wq * 32 + i * 16 + row) * LD + 8 * kq, fh[i]);
+    for (int ks = 0; ks < KSUB; ++ks) {
+      Frag<MMA> fa[2], fh[2];
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        gemm_frag<MMA>(As[buf] + (wm * 32 + i * 16 + row) * LD + 32 * ks + 8 * kq, fa[i]);
+        gemm_frag<MMA>(Hs[buf] + (wq * 32 + i * 16 + row) * LD + 32 * ks + 8 * kq, fh[i]);
+      }
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[i][j] = mma(fa[i], fh[j], acc[i][j]);
     }
-#pragma unroll
-    for (int i = 0; i < 2; ++i)
-#pragma unroll
-      for (int j = 0; j < 2; ++j) acc[i][j] = mma(fa[i], fh[j], acc[i][j]);
     if (s + 1 < s_hi) stage(buf ^ 1);
     __syncthreads();
   }
@@ -207,8 +259,8 @@ __global__ void __launch_bounds__(256) clear_kernel(uint32_t* p, long n) {
 
 template <int MMA>
 static const void* gemm_of(bool wide) {
-  return wide ? reinterpret_cast<const void*>(&dr_gemm_kernel<MMA, 2, 2>)
-              : reinterpret_cast<const void*>(&dr_gemm_kernel<MMA, 1, 1>);
+  return wide ? reinterpret_cast<const void*>(&dr_gemm_kernel<MMA, 2, 2, 1>)
+              : reinterpret_cast<const void*>(&dr_gemm_kernel<MMA, 1, 1, 1>);
 }
 const void* gemm_kernel(int mma, bool wide) {
   switch (mma) {
