@@ -51,6 +51,7 @@ EXPORTS = (
     "frnn_strerror",
     "frnn_set_spin_limit",
     "frnn_set_scouts",
+    "frnn_set_gemm_dma",
     "frnn_timing_enable",
     "frnn_timing_read",
     "frnn_set_phase_profile",
@@ -89,6 +90,8 @@ def load(path: str | os.PathLike | None = None) -> ctypes.CDLL:
     lib.frnn_set_spin_limit.restype = None
     lib.frnn_set_scouts.argtypes = [i32]
     lib.frnn_set_scouts.restype = None
+    lib.frnn_set_gemm_dma.argtypes = [i32]
+    lib.frnn_set_gemm_dma.restype = None
     lib.frnn_timing_enable.argtypes = [i32]
     lib.frnn_timing_enable.restype = None
     lib.frnn_timing_read.argtypes = [ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_int32)]

@@ -21,6 +21,11 @@ using frnn::Plan;
 
 constexpr uint32_t kDefaultSpinLimit = 1u << 22;
 std::atomic<uint32_t> g_spin_limit{kDefaultSpinLimit};
+// FRNN_NO_GEMM_DMA=1 (environment, read once): the dR GEMM's register-staged kernel only.
+std::atomic<bool> g_no_gemm_dma{[] {
+  const char* e = std::getenv("FRNN_NO_GEMM_DMA");
+  return e && *e && *e != '0';
+}()};
 // FRNN_NO_SCOUT=1 (environment, read once): no L2-prefetch workgroups in the backward.
 std::atomic<bool> g_no_scout{[] {
   const char* e = std::getenv("FRNN_NO_SCOUT");
@@ -218,7 +223,7 @@ int make_plan(const frnn_desc* d, Plan* p) {
   p->off_claim_f = align_up(p->off_x + 2 * p->xwords_fwd * wsz);
   p->ws_fwd = align_up(p->off_claim_f + nclaim);
   p->off_claim_b = align_up(p->off_x + 2 * p->xwords_bwd * wsz);
-  p->off_dcand = align_up(p->off_claim_b + nclaim);
+  p->off_dcand = align_up(p->off_claim_b + nclaim + 256);  // + 256 zero bytes (dR GEMM's DMA tail source)
   const long long ndcand = p->cell == FRNN_GRU ? (long long)p->B * p->T * p->N * p->D : 0;
   p->off_part = align_up(p->off_dcand + ndcand * 4);
   p->off_dbpart = align_up(p->off_part + (long long)p->splitk * p->N * p->GR * p->D * p->D * 4);
@@ -451,13 +456,17 @@ int frnn_bwd(const frnn_desc* d, const void* R, const void* s0, const void* stat
   g.s0 = s0;
   g.part = reinterpret_cast<float*>(w + p.off_part);
   g.dbpart = a.dbpart;
+  g.zero = w + p.off_claim_b + 2LL * p.ngroups * frnn::kXcds * 4;
   g.dR = dR;
   g.db = db;
   const bool wide = p.D % 64 == 0;
   const int tile = wide ? 64 : 32;
   const long long gwg = (long long)p.N * (p.GR * p.D / tile) * (p.D / tile) * p.splitk;
   timed = timing_begin(st, &t0);
-  rc = launch(frnn::gemm_kernel(p.mma, wide), (int)gwg, wide ? 256 : 64, 0, &g, st);
+  const int h16 = p.mma == FRNN_MMA_BF16 ? FRNN_BF16 : (p.mma == FRNN_MMA_F16 ? FRNN_F16 : -1);
+  const bool dma = wide && p.cell != FRNN_GRU && h16 >= 0 && p.dt_io == h16 && p.dt_out == h16 && p.dt_state == h16 &&
+                   !g_no_gemm_dma.load();
+  rc = launch(dma ? frnn::gemm_dma_kernel(p.mma) : frnn::gemm_kernel(p.mma, wide), (int)gwg, wide ? 256 : 64, 0, &g, st);
   const long long nout = (long long)p.N * p.GR * p.D * p.D + (long long)p.GT * p.N * p.D;
   const int rgrid = (int)std::min<long long>(4096, (nout + 255) / 256);
   if (rc == FRNN_OK) rc = launch(frnn::reduce_kernel(), rgrid, 256, 0, &g, st);
@@ -518,5 +527,7 @@ void frnn_set_phase_profile(void* device_words) {
 void frnn_set_spin_limit(uint32_t polls) { g_spin_limit.store(polls ? polls : kDefaultSpinLimit); }
 
 void frnn_set_scouts(int enable) { g_no_scout.store(enable == 0); }
+
+void frnn_set_gemm_dma(int enable) { g_no_gemm_dma.store(enable == 0); }
 
 }  // extern "C"

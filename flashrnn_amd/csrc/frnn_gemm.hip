@@ -228,6 +228,123 @@ __global__ void __launch_bounds__(64 * WM * WQ) dr_gemm_kernel(GemmArgs a) {
         out[(long)(m0 + wm * 32 + i * 16 + 4 * kq + r) * p.D + q0 + wq * 32 + j * 16 + row] = acc[i][j][r];
 }
 
+// The same 64x64 tiles and split-K stages of 32 k, with the operand tiles
+// loaded by LDS-DMA (global_load_lds: no registers in flight) into a ring of
+// kGemmRing stages, kGemmRing - 1 stages ahead of their use: the register-
+// staged kernel above waits a full load latency per stage. Wave w loads rows
+// 8w .. 8w+7 of a stage (k = 32 s + 8w + lane / 8, 16 bytes = 8 columns per
+// lane) of both operands, straight from dWx and from the state output (s0 for
+// t = 0) in their [k][column] layout; a rows beyond B*T reads 16 zero bytes.
+// A fragment then gathers its 8 consecutive k of one column with 16-bit LDS
+// reads (one per k), which a row-major tile needs. Same stages, same k
+// grouping per MFMA, so the result is bitwise that of the kernel above.
+constexpr int kGemmRing = 4;
+constexpr int kGemmGroup = 8 * 128 + 64;                 // bytes per 8-row group (+ pad against bank conflicts)
+constexpr int kGemmSlot = 2 * 4 * kGemmGroup;            // A and h, four groups each
+
+template <int MMA>
+__device__ __forceinline__ Frag<MMA> gemm_gather(const char* grp, int col) {
+  // 8 k (rows j of the 8-row group) of column col, packed two per dword
+  typedef int i32x4 __attribute__((ext_vector_type(4)));
+  i32x4 v;
+#pragma unroll
+  for (int j = 0; j < 8; j += 2) {
+    const uint32_t lo = *reinterpret_cast<const unsigned short*>(grp + j * 128 + 2 * col);
+    const uint32_t hi = *reinterpret_cast<const unsigned short*>(grp + (j + 1) * 128 + 2 * col);
+    v[j / 2] = (int)(lo | (hi << 16));
+  }
+  Frag<MMA> f;
+  if constexpr (MMA == MMA_BF16) f.v = __builtin_bit_cast(bf16x8, v);
+  else f.v = __builtin_bit_cast(f16x8, v);
+  return f;
+}
+
+template <int MMA>
+__global__ void __launch_bounds__(256) dr_gemm_dma_kernel(GemmArgs a) {
+  static_assert(MMA != MMA_F32, "16-bit operands only");
+  __shared__ __attribute__((aligned(16))) char ring[kGemmRing * kGemmSlot];
+  const Plan& p = a.p;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int GD = p.GR * p.D;
+  const int mt = GD / 64, qt = p.D / 64;
+  const int tiles = p.N * mt * qt;
+  const int full = (int)(gridDim.x / kXcds) * kXcds, bx = blockIdx.x;
+  const int tile_id = bx < full ? (bx % kXcds) * (full / kXcds) + bx / kXcds : bx;
+  const int split = tile_id / tiles;
+  int rem = tile_id % tiles;
+  const int n = rem / (mt * qt);
+  rem %= mt * qt;
+  const int m0 = (rem % mt) * 64, q0 = (rem / mt) * 64;
+  const long K = (long)p.B * p.T;
+  const long KT = (K + 31) / 32;
+  const long s_lo = KT * split / p.splitk, s_hi = KT * (split + 1) / p.splitk;
+  const int row = lane & 15, kq = lane >> 4;
+  const int wm = w & 1, wq = w >> 1;
+
+  // this lane's DMA row: k = 32 s + 8 w + lane / 8, columns 8 (lane % 8) .. +7
+  const int g = m0 / p.D, o = m0 % p.D + 8 * (lane & 7), q = q0 + 8 * (lane & 7);
+  const long wxt = (long)p.GW * p.N * p.D;
+  const char* abase = static_cast<const char*>(a.dwx) + (((long)g * p.N + n) * p.D + o) * 2;
+  const char* sbase = static_cast<const char*>(a.states) + ((long)n * p.D + q) * 2;  // + ((b T + t - 1) N D) * 2
+  const char* s0base = static_cast<const char*>(a.s0) + ((long)n * p.D + q) * 2;     // + (b N D) * 2
+  long k = 32 * s_lo + 8 * w + (lane >> 3);
+  int b = (int)(k / p.T), t = (int)(k % p.T);
+  auto issue = [&](long s) {  // DMA of stage s into its ring slot; advances this lane's row
+    char* slot = ring + (int)(s % kGemmRing) * kGemmSlot;
+    const char* src_a = static_cast<const char*>(a.zero);
+    const char* src_h = static_cast<const char*>(a.zero);
+    if (b < p.B) {
+      src_a = abase + ((long)b * p.T + t) * wxt * 2;
+      src_h = t > 0 ? sbase + ((long)b * p.T + t - 1) * p.N * p.D * 2 : s0base + (long)b * p.N * p.D * 2;
+    }
+    __builtin_amdgcn_global_load_lds(src_a, (__attribute__((address_space(3))) void*)(slot + w * kGemmGroup), 16, 0, 0);
+    __builtin_amdgcn_global_load_lds(src_h, (__attribute__((address_space(3))) void*)(slot + (4 + w) * kGemmGroup), 16,
+                                     0, 0);
+    t += 32;
+    while (t >= p.T) {
+      t -= p.T;
+      ++b;
+    }
+  };
+
+  f32x4 acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  constexpr int AHEAD = kGemmRing - 1;
+  for (long s = s_lo; s < s_lo + AHEAD && s < s_hi; ++s) issue(s);
+  for (long s = s_lo; s < s_hi; ++s) {
+    // this wave's loads of stage s have landed: 2 DMAs per later stage may still fly
+    if (s + AHEAD <= s_hi) wait_vm<2 * (AHEAD - 1)>();
+    else wait_vm<0>();
+    // every wave's loads of stage s landed; everyone done with stage s-1 (a
+    // plain barrier: a fence here would also wait for the later stages' DMA)
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    if (s + AHEAD < s_hi) issue(s + AHEAD);  // into the slot of stage s-1
+    const char* slot = ring + (int)(s % kGemmRing) * kGemmSlot;
+    Frag<MMA> fa[2], fh[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      fa[i] = gemm_gather<MMA>(slot + kq * kGemmGroup, wm * 32 + i * 16 + row);
+      fh[i] = gemm_gather<MMA>(slot + (4 + kq) * kGemmGroup, wq * 32 + i * 16 + row);
+    }
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) acc[i][j] = mma(fa[i], fh[j], acc[i][j]);
+  }
+  float* out = a.part + ((long)split * p.N + n) * GD * p.D;
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        out[(long)(m0 + wm * 32 + i * 16 + 4 * kq + r) * p.D + q0 + wq * 32 + j * 16 + row] = acc[i][j][r];
+}
+
 // dR = sum of the split-K partials (layout [n][g*D+o][p] -> [g][n][o][p]);
 // db = sum of the per-group partials over slabs and batch rows.
 __global__ void __launch_bounds__(256) dr_reduce_kernel(GemmArgs a) {
@@ -267,6 +384,13 @@ const void* gemm_kernel(int mma, bool wide) {
     case MMA_BF16: return gemm_of<MMA_BF16>(wide);
     case MMA_F16: return gemm_of<MMA_F16>(wide);
     case MMA_F32: return gemm_of<MMA_F32>(wide);
+  }
+  return nullptr;
+}
+const void* gemm_dma_kernel(int mma) {
+  switch (mma) {
+    case MMA_BF16: return reinterpret_cast<const void*>(&dr_gemm_dma_kernel<MMA_BF16>);
+    case MMA_F16: return reinterpret_cast<const void*>(&dr_gemm_dma_kernel<MMA_F16>);
   }
   return nullptr;
 }

@@ -54,7 +54,13 @@ struct GemmArgs {
   const float* dbpart;
   void* dR;
   void* db;
+  const void* zero;  // 256 zero bytes (the DMA path's source for k beyond B*T)
 };
+
+// dR GEMM whose operand tiles are loaded by LDS-DMA several stages ahead: 16-bit
+// operands already in the MMA's type (dWx, states and s0 alike), D % 64 == 0, not
+// the GRU (whose candidate gate comes from an FP32 buffer); null otherwise.
+const void* gemm_dma_kernel(int mma);
 
 // Persistent recurrence kernel for (mma, k-tiles per wave) of one cell; null if not built.
 const void* lstm_kernel(int mma, int ks, int ktw, int ndt, bool forward);

@@ -469,14 +469,6 @@ __device__ __forceinline__ uint32_t gather_pair_mma(const Xchg& x, const int (&w
 // vector access and every LDS access one 16-byte access.
 __device__ __forceinline__ int io_elem(int lane, int i) { return 256 * (i >> 2) + 4 * lane + (i & 3); }
 
-// s_waitcnt that waits until at most n vector-memory operations of this wave
-// are outstanding (gfx9 encoding: vmcnt in bits 3:0 and 15:14; expcnt and
-// lgkmcnt left at their maxima, i.e. not waited for).
-template <int n>
-__device__ __forceinline__ void wait_vm() {
-  static_assert(n >= 0 && n < 64, "vmcnt range");
-  __builtin_amdgcn_s_waitcnt((n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8));
-}
 
 // I/O wave of a team. Wx of step u is loaded straight into raw slot u % 2 by
 // LDS-DMA (global_load_lds: no registers in flight), three steps ahead; two

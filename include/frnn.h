@@ -190,6 +190,12 @@ void frnn_set_spin_limit(uint32_t polls);
  * extra launch and get a CU to themselves. */
 void frnn_set_scouts(int enable);
 
+/* Tuning hook, no counterpart in the reference: enable (1, the default unless the
+ * environment sets FRNN_NO_GEMM_DMA=1) or disable (0) the dR GEMM whose operand tiles
+ * are loaded by LDS-DMA (used for 16-bit operands already in the MMA type and D % 64 == 0,
+ * not the GRU). Both kernels give bitwise the same dR. */
+void frnn_set_gemm_dma(int enable);
+
 #ifdef __cplusplus
 }
 #endif

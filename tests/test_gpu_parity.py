@@ -136,3 +136,34 @@ def test_scouts_change_timing_only(cell, B):
         lib.frnn_set_scouts(1)
     for a, b in zip(*outs):
         assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("cell,B,T,N,D", [("lstm", 8, 64, 3, 256), ("slstm", 5, 40, 2, 128), ("elman", 16, 33, 1, 192),
+                                          ("lstm", 3, 7, 2, 64)])
+def test_dr_gemm_dma_path(cell, B, T, N, D):
+    """All-BF16 inputs (s0 too) take the LDS-DMA dR GEMM: bitwise the register-staged GEMM's
+    dR, and within tolerance of the oracle."""
+    from flashrnn_amd import _lib, flashrnn, set_strict
+
+    set_strict(True)
+    cpu, dh, dl = make(cell, B, T, N, D, seed=11)
+    cpu = tuple(t.to(torch.bfloat16).float() for t in cpu)
+    leaves = [t.clone().requires_grad_() for t in cpu]
+    eh, el = flashrnn_torch(*leaves, cell=cell, numerics="fp32_state_bf16_mma")
+    eg = torch.autograd.grad((eh * dh).sum() + (el * dl).sum(), leaves)
+    lib = _lib.load()
+    grads = []
+    try:
+        for on in (1, 0):
+            lib.frnn_set_gemm_dma(on)
+            gl = [t.to("cuda", torch.bfloat16).requires_grad_() for t in cpu]
+            ah, al = flashrnn(*gl, function=cell, dtype="bfloat16")
+            ag = torch.autograd.grad((ah.float() * dh.cuda()).sum() + (al.float() * dl.cuda()).sum(), gl)
+            torch.cuda.synchronize()
+            grads.append([t.detach().cpu() for t in ag])
+    finally:
+        lib.frnn_set_gemm_dma(1)
+    for a, b in zip(*grads):
+        assert torch.equal(a, b)
+    for name, a, e in zip(("dWx", "dR", "db", "ds0"), grads[0], eg):
+        assert rel(a, e) <= 1e-2, (name, rel(a, e))
