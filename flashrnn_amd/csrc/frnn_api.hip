@@ -205,13 +205,14 @@ int make_plan(const frnn_desc* d, Plan* p) {
   p->xwords_bwd = (long long)p->ngroups * p->BS * p->GR * p->D;
   p->save_floats = (long long)p->T * p->nwg * p->nsave * p->NDT * 256 * p->NB;
   // dR GEMM: 64x64 workgroup tiles where D % 64 == 0 (else 32x32), split over
-  // K = B*T to fill the GPU (~4096 workgroups, >= 8 k-steps of 32 each): the
-  // GEMM is bound by its operand-load latency, so more workgroups in flight win
-  // over the larger split-K reduction (measured 0.153 -> 0.138 ms at C2)
+  // K = B*T to fill the GPU (~2048 workgroups, >= 8 k-steps of 32 each): the
+  // GEMM is bound by its operand-load latency, so more workgroups in flight
+  // pay for the larger split-K reduction (measured at B8 T1024 N3 D256 and at
+  // B256 T1024 N8 D128 with the LDS-DMA GEMM: 1024, 2048 and 4096 workgroups)
   const int tile = p->D % 64 == 0 ? 64 : 32;
   const long long tiles = (long long)p->N * (p->GR * p->D / tile) * (p->D / tile);
   const long long ktt = ((long long)p->B * p->T + 31) / 32;
-  long long split = std::max<long long>(1, 4096 / std::max<long long>(1, tiles));
+  long long split = std::max<long long>(1, 2048 / std::max<long long>(1, tiles));
   split = std::min<long long>(split, std::max<long long>(1, ktt / 8));
   p->splitk = (int)std::min<long long>(split, 64);
   // saved-for-backward area: the lane-native values only
