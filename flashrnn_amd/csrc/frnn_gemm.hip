@@ -370,6 +370,12 @@ __global__ void __launch_bounds__(256) dr_reduce_kernel(GemmArgs a) {
   }
 }
 
+// FP32 -> 16-bit (dt: BF16 or FP16) bits, round to nearest even.
+__global__ void __launch_bounds__(256) to16_copy_kernel(const float* src, unsigned short* dst, long n, int dt) {
+  for (long i = blockIdx.x * 256L + threadIdx.x; i < n; i += (long)gridDim.x * 256)
+    dst[i] = (unsigned short)h16_bits(src[i], dt);
+}
+
 __global__ void __launch_bounds__(256) clear_kernel(uint32_t* p, long n) {
   for (long i = blockIdx.x * 256L + threadIdx.x; i < n; i += (long)gridDim.x * 256) p[i] = 0u;
 }
@@ -396,5 +402,6 @@ const void* gemm_dma_kernel(int mma) {
 }
 const void* reduce_kernel() { return reinterpret_cast<const void*>(&dr_reduce_kernel); }
 const void* zero_kernel() { return reinterpret_cast<const void*>(&clear_kernel); }
+const void* to16_kernel() { return reinterpret_cast<const void*>(&to16_copy_kernel); }
 
 }  // namespace frnn

@@ -61,6 +61,8 @@ struct GemmArgs {
 // operands already in the MMA's type (dWx, states and s0 alike), D % 64 == 0, not
 // the GRU (whose candidate gate comes from an FP32 buffer); null otherwise.
 const void* gemm_dma_kernel(int mma);
+// FP32 -> 16-bit copy (the DMA GEMM's h_{-1} rows when s0 is FP32).
+const void* to16_kernel();
 
 // Persistent recurrence kernel for (mma, k-tiles per wave) of one cell; null if not built.
 const void* lstm_kernel(int mma, int ks, int ktw, int ndt, bool forward);

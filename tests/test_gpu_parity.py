@@ -140,9 +140,10 @@ def test_scouts_change_timing_only(cell, B):
 
 @pytest.mark.parametrize("cell,B,T,N,D", [("lstm", 8, 64, 3, 256), ("slstm", 5, 40, 2, 128), ("elman", 16, 33, 1, 192),
                                           ("lstm", 3, 7, 2, 64)])
-def test_dr_gemm_dma_path(cell, B, T, N, D):
-    """All-BF16 inputs (s0 too) take the LDS-DMA dR GEMM: bitwise the register-staged GEMM's
-    dR, and within tolerance of the oracle."""
+@pytest.mark.parametrize("s0_f32", [False, True])
+def test_dr_gemm_dma_path(cell, B, T, N, D, s0_f32):
+    """BF16 inputs take the LDS-DMA dR GEMM (an FP32 s0 through a rounded BF16 copy): bitwise
+    the register-staged GEMM's dR, and within tolerance of the oracle."""
     from flashrnn_amd import _lib, flashrnn, set_strict
 
     set_strict(True)
@@ -157,6 +158,8 @@ def test_dr_gemm_dma_path(cell, B, T, N, D):
         for on in (1, 0):
             lib.frnn_set_gemm_dma(on)
             gl = [t.to("cuda", torch.bfloat16).requires_grad_() for t in cpu]
+            if s0_f32:
+                gl[3] = cpu[3].to("cuda").requires_grad_()
             ah, al = flashrnn(*gl, function=cell, dtype="bfloat16")
             ag = torch.autograd.grad((ah.float() * dh.cuda()).sum() + (al.float() * dl.cuda()).sum(), gl)
             torch.cuda.synchronize()
