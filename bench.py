@@ -153,7 +153,47 @@ def extras(torch, dev, flashrnn):
         "workload": "LSTM B8 T1024 N3 D256 bf16, forward only, hidden output, HIP graph",
         "ms": ms, "timesteps_batch_per_s": round(B * T / (ms / 1e3), 1),
     }
+    out["other_configs"] = other_configs(torch, dev, flashrnn)
     return out
+
+
+# BASELINE configs[2:] (parity cases in tests/; timed here as side measurements):
+# cell, B, T, N, D, chunks (chunks > 1: the sequence runs as that many calls, each
+# chunk's last state the next chunk's initial state, gradients through all of them)
+OTHER_CONFIGS = [("gru", 16, 512, 1, 768, 1), ("elman", 16, 512, 1, 768, 1), ("slstm", 16, 2048, 4, 192, 1),
+                 ("lstm", 256, 1024, 8, 128, 4)]
+
+
+def other_configs(torch, dev, flashrnn):
+    """fwd+bwd wall time (median of 10, bf16 operands, FP32 state) of the other BASELINE configs."""
+    gates = {"lstm": (4, 4, 4, 2), "gru": (3, 3, 4, 1), "elman": (1, 1, 1, 1), "slstm": (4, 4, 4, 4)}
+    res = []
+    for cell, b_, t_, n_, d_, chunks in OTHER_CONFIGS:
+        gr, gw, gt, s_ = gates[cell]
+        g = torch.Generator().manual_seed(3)
+        tc = t_ // chunks
+        wx = torch.randn(b_, t_, gw, n_, d_, generator=g).to(dev, torch.bfloat16)
+        wxs = [wx[:, c * tc:(c + 1) * tc].contiguous().requires_grad_() for c in range(chunks)]
+        R = (torch.randn(gr, n_, d_, d_, generator=g) / d_**0.5).to(dev, torch.bfloat16).requires_grad_()
+        bias = 0.1 * torch.randn(gt, n_, d_, generator=g)
+        if cell == "slstm":
+            bias[1] = 3 + 3 * torch.rand(n_, d_, generator=g)
+        bias = bias.to(dev, torch.bfloat16).requires_grad_()
+        s0 = torch.zeros(s_, b_, 1, n_, d_, device=dev, requires_grad=True)
+        dh = torch.randn(s_, b_, tc, n_, d_, generator=g).to(dev, torch.bfloat16)
+
+        def fwdbwd():
+            state, loss = s0, 0.0
+            for c in range(chunks):
+                h, state = flashrnn(wxs[c], R, bias, state, function=cell, dtype="bfloat16")
+                loss = loss + (h.float() * dh).sum()
+            loss = loss + state.float().sum()
+            torch.autograd.grad(loss, (*wxs, R, bias, s0))
+
+        ms = _time_ms(torch, fwdbwd, reps=10, warmup=2)
+        res.append({"workload": f"{cell} B{b_} T{t_} N{n_} D{d_}" + (f" in {chunks} chunks" if chunks > 1 else ""),
+                    "fwd_bwd_ms": ms, "timesteps_batch_per_s": round(b_ * t_ / (ms / 1e3), 1)})
+    return res
 
 
 def main(argv=None):
