@@ -133,8 +133,12 @@ void set_groups(Plan* p, int g0, int n) {
                                                 frnn::scout_blocks(*p);
 }
 
-// Bytes at the end of the backward workspace for a 16-bit copy of s0[0] ([B][N][D]).
+// Bytes at the end of the backward workspace for a 16-bit copy of s0[0] ([B][N][D])
+// and, for the GRU, of the candidate-gate cotangents ([B][T][N][D]).
 long long s0_copy_bytes(const Plan& p) { return align_up((long long)p.B * p.N * p.D * 2); }
+long long cand_copy_bytes(const Plan& p) {
+  return p.cell == FRNN_GRU ? align_up((long long)p.B * p.T * p.N * p.D * 2) : 0;
+}
 
 int make_plan(const frnn_desc* d, Plan* p) {
   if (!d) return FRNN_E_INVALID;
@@ -233,7 +237,7 @@ int make_plan(const frnn_desc* d, Plan* p) {
   p->off_dbpart = align_up(p->off_part + (long long)p->splitk * p->N * p->GR * p->D * p->D * 4);
   p->ws_bwd = align_up(p->off_dbpart + (long long)p->ngroups * p->GT * p->BS * p->D * 4);
   // last: a 16-bit copy of an FP32 initial hidden state, for the LDS-DMA dR GEMM
-  p->ws_bwd += s0_copy_bytes(*p);
+  p->ws_bwd += s0_copy_bytes(*p) + cand_copy_bytes(*p);
   if (2 * p->xwords_bwd * wsz > 0x7fffffffLL) return FRNN_E_UNSUPPORTED;  // buffer-descriptor range
   return FRNN_OK;
 }
@@ -470,23 +474,28 @@ int frnn_bwd(const frnn_desc* d, const void* R, const void* s0, const void* stat
   const long long gwg = (long long)p.N * (p.GR * p.D / tile) * (p.D / tile) * p.splitk;
   timed = timing_begin(st, &t0);
   const int h16 = p.mma == FRNN_MMA_BF16 ? FRNN_BF16 : (p.mma == FRNN_MMA_F16 ? FRNN_F16 : -1);
-  const bool dma = wide && p.cell != FRNN_GRU && h16 >= 0 && p.dt_io == h16 && p.dt_out == h16 &&
+  const bool dma = wide && h16 >= 0 && p.dt_io == h16 && p.dt_out == h16 &&
                    (p.dt_state == h16 || p.dt_state == FRNN_F32) && !g_no_gemm_dma.load();
+  // FP32 -> MMA-type copy (rounded as the register-staged GEMM rounds its operands)
+  auto to16 = [&](const float* src, unsigned short* dst, long n16) {
+    int dt = h16;
+    void* cargs[] = {&src, &dst, &n16, &dt};
+    return hipLaunchKernel(frnn::to16_kernel(), dim3((unsigned)std::min<long>(2048, (n16 + 255) / 256)), dim3(256), cargs,
+                           0, st) == hipSuccess;
+  };
+  char* copies = w + p.ws_bwd - s0_copy_bytes(p) - cand_copy_bytes(p);
   if (dma && p.dt_state == FRNN_F32) {
-    // the GEMM's h_{-1} rows: s0[0] rounded to the MMA type, as the other GEMM rounds it
-    unsigned short* s0h = reinterpret_cast<unsigned short*>(w + p.ws_bwd - s0_copy_bytes(p));
-    const long n16 = (long)p.B * p.N * p.D;
-    struct {
-      const float* src;
-      unsigned short* dst;
-      long n;
-      int dt;
-    } c{static_cast<const float*>(s0), s0h, n16, h16};
-    void* cargs[] = {&c.src, &c.dst, &c.n, &c.dt};
-    if (hipLaunchKernel(frnn::to16_kernel(), dim3((unsigned)std::min<long>(1024, (n16 + 255) / 256)), dim3(256), cargs, 0,
-                        st) != hipSuccess)
-      return FRNN_E_LAUNCH;
+    // the GEMM's h_{-1} rows: s0[0] in the MMA type
+    unsigned short* s0h = reinterpret_cast<unsigned short*>(copies + cand_copy_bytes(p));
+    if (!to16(static_cast<const float*>(s0), s0h, (long)p.B * p.N * p.D)) return FRNN_E_LAUNCH;
     g.s0 = s0h;
+  }
+  g.dcand16 = nullptr;
+  if (dma && p.cell == FRNN_GRU) {
+    // the candidate gate's A rows: its FP32 cotangents in the MMA type
+    unsigned short* ch = reinterpret_cast<unsigned short*>(copies);
+    if (!to16(a.dcand, ch, (long)p.B * p.T * p.N * p.D)) return FRNN_E_LAUNCH;
+    g.dcand16 = ch;
   }
   rc = launch(dma ? frnn::gemm_dma_kernel(p.mma) : frnn::gemm_kernel(p.mma, wide), (int)gwg, wide ? 256 : 64, 0, &g, st);
   const long long nout = (long long)p.N * p.GR * p.D * p.D + (long long)p.GT * p.N * p.D;

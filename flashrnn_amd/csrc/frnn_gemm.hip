@@ -283,8 +283,12 @@ __global__ void __launch_bounds__(256) dr_gemm_dma_kernel(GemmArgs a) {
 
   // this lane's DMA row: k = 32 s + 8 w + lane / 8, columns 8 (lane % 8) .. +7
   const int g = m0 / p.D, o = m0 % p.D + 8 * (lane & 7), q = q0 + 8 * (lane & 7);
-  const long wxt = (long)p.GW * p.N * p.D;
-  const char* abase = static_cast<const char*>(a.dwx) + (((long)g * p.N + n) * p.D + o) * 2;
+  // A rows: dWx at gate g (GRU: gate g - 1 of dWx, gate 0 the candidate cotangents)
+  const bool cand = p.cell == CELL_GRU && g == 0;
+  const long wxt = cand ? (long)p.N * p.D : (long)p.GW * p.N * p.D;  // elements per (b, t)
+  const char* abase = cand ? static_cast<const char*>(a.dcand16) + ((long)n * p.D + o) * 2
+                           : static_cast<const char*>(a.dwx) +
+                                 (((long)(p.cell == CELL_GRU ? g - 1 : g) * p.N + n) * p.D + o) * 2;
   const char* sbase = static_cast<const char*>(a.states) + ((long)n * p.D + q) * 2;  // + ((b T + t - 1) N D) * 2
   const char* s0base = static_cast<const char*>(a.s0) + ((long)n * p.D + q) * 2;     // + (b N D) * 2
   long k = 32 * s_lo + 8 * w + (lane >> 3);

@@ -54,7 +54,8 @@ struct GemmArgs {
   const float* dbpart;
   void* dR;
   void* db;
-  const void* zero;  // 256 zero bytes (the DMA path's source for k beyond B*T)
+  const void* zero;     // 256 zero bytes (the DMA path's source for k beyond B*T)
+  const void* dcand16;  // GRU, DMA path: dcand in the MMA type
 };
 
 // dR GEMM whose operand tiles are loaded by LDS-DMA several stages ahead: 16-bit

@@ -139,10 +139,11 @@ def test_scouts_change_timing_only(cell, B):
 
 
 @pytest.mark.parametrize("cell,B,T,N,D", [("lstm", 8, 64, 3, 256), ("slstm", 5, 40, 2, 128), ("elman", 16, 33, 1, 192),
-                                          ("lstm", 3, 7, 2, 64)])
+                                          ("lstm", 3, 7, 2, 64), ("gru", 3, 7, 2, 64), ("gru", 16, 16, 1, 768)])
 @pytest.mark.parametrize("s0_f32", [False, True])
 def test_dr_gemm_dma_path(cell, B, T, N, D, s0_f32):
-    """BF16 inputs take the LDS-DMA dR GEMM (an FP32 s0 through a rounded BF16 copy): bitwise
+    """BF16 inputs take the LDS-DMA dR GEMM (an FP32 s0, and the GRU's FP32 candidate-gate
+    cotangents, through rounded BF16 copies): bitwise
     the register-staged GEMM's dR, and within tolerance of the oracle."""
     from flashrnn_amd import _lib, flashrnn, set_strict
 
