@@ -57,12 +57,43 @@ def make_inputs(torch, device, seed=20261201):
     return (wx, R, b, s0), (dh, dl)
 
 
+def physical_cores(cap=16):
+    """Physical cores of this process's CPU set (distinct (package, core) pairs, SMT siblings
+    counted once), at most `cap` (the GPU box's CPU share), and a description of the host
+    from lscpu (sockets x cores per socket x threads per core)."""
+    cpus = sorted(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else list(range(os.cpu_count() or 1))
+    pairs = set()
+    for c in cpus:
+        base = f"/sys/devices/system/cpu/cpu{c}/topology/"
+        try:
+            pkg = open(base + "physical_package_id").read().strip()
+            core = open(base + "core_id").read().strip()
+            pairs.add((pkg, core))
+        except OSError:
+            pairs.add(("cpu", str(c)))
+    host = f"{len(cpus)} logical CPUs in the process's set"
+    try:
+        import subprocess
+
+        info = dict(
+            (k.strip(), v.strip())
+            for k, v in (ln.split(":", 1) for ln in subprocess.run(["lscpu"], capture_output=True, text=True,
+                                                                     timeout=10).stdout.splitlines() if ":" in ln)
+        )
+        host = (f"lscpu: {info.get('Model name', '?')}, {info.get('Socket(s)', '?')} socket(s) x "
+                f"{info.get('Core(s) per socket', '?')} cores x {info.get('Thread(s) per core', '?')} threads; "
+                f"{len(cpus)} logical CPUs / {len(pairs)} physical cores in the process's set")
+    except (OSError, ValueError, subprocess.SubprocessError):
+        pass
+    return max(1, min(cap, len(pairs))), host
+
+
 def cpu_baseline(torch, budget_s=30.0):
     """The CPU oracle at the full workload shape: median of fwd+bwd runs over about 10 s of CPU
     work (at least 3 runs, at most budget_s)."""
     from oracle.torch_restatement import flashrnn_torch
 
-    cores = min(16, os.cpu_count() or 1)
+    cores, host = physical_cores()
     torch.set_num_threads(cores)
     (wx, R, b, s0), (dh, dl) = make_inputs(torch, "cpu")
     leaves = [t.bfloat16().float().requires_grad_() for t in (wx, R, b, s0)]
@@ -85,7 +116,8 @@ def cpu_baseline(torch, budget_s=30.0):
         "kind": "port",
         "sample": f"full workload shape (B8 T1024 N3 D256 LSTM fwd+bwd), FP32 CPU oracle "
         f"(restated flashrnn_torch, numerics=fp32_state_bf16_mma), median of {len(times)} runs "
-        f"({times[0]:.2f}-{times[-1]:.2f} s each, {sum(times):.1f} s in all)",
+        f"({times[0]:.2f}-{times[-1]:.2f} s each, {sum(times):.1f} s in all); one thread per physical "
+        f"core of this process's CPU set; host: {host}",
     }
 
 

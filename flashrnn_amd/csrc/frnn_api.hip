@@ -133,11 +133,26 @@ void set_groups(Plan* p, int g0, int n) {
                                                 frnn::scout_blocks(*p);
 }
 
-// Bytes at the end of the backward workspace for a 16-bit copy of s0[0] ([B][N][D])
-// and, for the GRU, of the candidate-gate cotangents ([B][T][N][D]).
-long long s0_copy_bytes(const Plan& p) { return align_up((long long)p.B * p.N * p.D * 2); }
+// MMA-type dtype of a 16-bit policy, or -1 (FP32 operands).
+int mma_h16(int mma) { return mma == FRNN_MMA_BF16 ? FRNN_BF16 : (mma == FRNN_MMA_F16 ? FRNN_F16 : -1); }
+
+// Whether the backward's dR GEMM runs on the LDS-DMA kernel: 16-bit operands
+// already in the MMA's type (dWx and the state history; s0 in that type or FP32),
+// 64-wide tiles, and the kernel not switched off.
+bool gemm_uses_dma(const Plan& p) {
+  const int h16 = mma_h16(p.mma);
+  return p.D % 64 == 0 && h16 >= 0 && p.dt_io == h16 && p.dt_out == h16 &&
+         (p.dt_state == h16 || p.dt_state == FRNN_F32) && !g_no_gemm_dma.load();
+}
+
+// Bytes at the end of the backward workspace, for the LDS-DMA dR GEMM only: a
+// 16-bit copy of an FP32 s0[0] ([B][N][D]) and, for the GRU, of the FP32
+// candidate-gate cotangents ([B][T][N][D]).
+long long s0_copy_bytes(const Plan& p) {
+  return p.dma_gemm && p.dt_state == FRNN_F32 ? align_up((long long)p.B * p.N * p.D * 2) : 0;
+}
 long long cand_copy_bytes(const Plan& p) {
-  return p.cell == FRNN_GRU ? align_up((long long)p.B * p.T * p.N * p.D * 2) : 0;
+  return p.dma_gemm && p.cell == FRNN_GRU ? align_up((long long)p.B * p.T * p.N * p.D * 2) : 0;
 }
 
 int make_plan(const frnn_desc* d, Plan* p) {
@@ -236,7 +251,9 @@ int make_plan(const frnn_desc* d, Plan* p) {
   p->off_part = align_up(p->off_dcand + ndcand * 4);
   p->off_dbpart = align_up(p->off_part + (long long)p->splitk * p->N * p->GR * p->D * p->D * 4);
   p->ws_bwd = align_up(p->off_dbpart + (long long)p->ngroups * p->GT * p->BS * p->D * 4);
-  // last: a 16-bit copy of an FP32 initial hidden state, for the LDS-DMA dR GEMM
+  // last, for the LDS-DMA dR GEMM only: 16-bit copies of an FP32 initial hidden
+  // state and of the GRU's FP32 candidate-gate cotangents
+  p->dma_gemm = gemm_uses_dma(*p) ? 1 : 0;
   p->ws_bwd += s0_copy_bytes(*p) + cand_copy_bytes(*p);
   if (2 * p->xwords_bwd * wsz > 0x7fffffffLL) return FRNN_E_UNSUPPORTED;  // buffer-descriptor range
   return FRNN_OK;
@@ -344,6 +361,49 @@ int clear(void* base, long long bytes, hipStream_t stream) {
              : FRNN_E_LAUNCH;
 }
 
+// Forward launch on a workspace whose layout the plan gives (exchange and slot
+// counters at their offsets from `w`; the status word is `status`, which the
+// workspace's first word is for frnn_fwd). Clears the exchange and the counters,
+// then launches the persistent kernel(s). Allocates nothing.
+int fwd_launch(const Plan& p, const void* wx, const void* R, const void* b, const void* s0, void* states_out,
+               void* carry_out, void* save, char* w, uint32_t* status, bool allow_timing, hipStream_t st) {
+  if (!wx || !R || !b || !s0 || !states_out) return FRNN_E_INVALID;
+  const bool training = (p.flags & FRNN_TRAINING) != 0;
+  if (training && !save) return FRNN_E_INVALID;
+  const void* fn =
+      frnn::recurrence_kernel(p.cell, p.mma, p.KS, ktw_class((p.kt_fwd + p.KS - 1) / p.KS, p.NDT), p.NDT, true);
+  if (!fn) return FRNN_E_UNSUPPORTED;
+  int rc;
+  const long long xbytes = 2 * p.xwords_fwd * (p.mma == FRNN_MMA_F32 ? 8 : 4);
+  if ((rc = clear(w + p.off_x, p.ws_fwd - p.off_x, st)) != FRNN_OK) return rc;  // exchange and claims
+  frnn::FwdArgs a;
+  a.p = p;
+  a.wx = wx;
+  a.R = R;
+  a.bias = b;
+  a.s0 = s0;
+  a.states = states_out;
+  a.carry = carry_out;
+  a.save = training ? static_cast<float*>(save) : nullptr;
+  a.xbuf = w + p.off_x;
+  a.xbytes = xbytes;
+  a.claim = reinterpret_cast<uint32_t*>(w + p.off_claim_f);
+  a.status = status;
+  a.spin_limit = g_spin_limit.load();
+  a.prof = g_phase_prof.load();
+  size_t lds = (size_t)p.NDT * frnn::recurrence_lds_floats(p.cell, true, p.KS) * sizeof(float);
+  const int block = 64 * p.NDT * (p.KS + 1);
+  int per_launch = 0;
+  if ((rc = set_lds_limit(fn, lds)) != FRNN_OK) return rc;
+  if ((rc = groups_per_launch(p, fn, block, lds, &per_launch)) != FRNN_OK) return rc;
+  use_scouts(p, fn, block, &lds, &a.p, &per_launch);
+  hipEvent_t t0;
+  const bool timed = allow_timing && timing_begin(st, &t0);
+  rc = launch_groups(&a.p, fn, block, lds, &a, per_launch, st);
+  if (timed) timing_end(0, t0, st);
+  return rc;
+}
+
 }  // namespace
 
 extern "C" {
@@ -375,43 +435,10 @@ int frnn_fwd(const frnn_desc* d, const void* wx, const void* R, const void* b, c
   Plan p;
   int rc = make_plan(d, &p);
   if (rc != FRNN_OK) return rc;
-  if (!wx || !R || !b || !s0 || !states_out || !ws) return FRNN_E_INVALID;
-  const bool training = (p.flags & FRNN_TRAINING) != 0;
-  if (training && !save) return FRNN_E_INVALID;
+  if (!ws) return FRNN_E_INVALID;
   if ((long long)ws_bytes < p.ws_fwd) return FRNN_E_WORKSPACE;
-  const void* fn =
-      frnn::recurrence_kernel(p.cell, p.mma, p.KS, ktw_class((p.kt_fwd + p.KS - 1) / p.KS, p.NDT), p.NDT, true);
-  if (!fn) return FRNN_E_UNSUPPORTED;
-  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  char* w = static_cast<char*>(ws);
-  const long long xbytes = 2 * p.xwords_fwd * (p.mma == FRNN_MMA_F32 ? 8 : 4);
-  if ((rc = clear(w + p.off_x, p.ws_fwd - p.off_x, st)) != FRNN_OK) return rc;  // exchange and claims
-  frnn::FwdArgs a;
-  a.p = p;
-  a.wx = wx;
-  a.R = R;
-  a.bias = b;
-  a.s0 = s0;
-  a.states = states_out;
-  a.carry = carry_out;
-  a.save = training ? static_cast<float*>(save) : nullptr;
-  a.xbuf = w + p.off_x;
-  a.xbytes = xbytes;
-  a.claim = reinterpret_cast<uint32_t*>(w + p.off_claim_f);
-  a.status = reinterpret_cast<uint32_t*>(w);
-  a.spin_limit = g_spin_limit.load();
-  a.prof = g_phase_prof.load();
-  size_t lds = (size_t)p.NDT * frnn::recurrence_lds_floats(p.cell, true, p.KS) * sizeof(float);
-  const int block = 64 * p.NDT * (p.KS + 1);
-  int per_launch = 0;
-  if ((rc = set_lds_limit(fn, lds)) != FRNN_OK) return rc;
-  if ((rc = groups_per_launch(p, fn, block, lds, &per_launch)) != FRNN_OK) return rc;
-  use_scouts(p, fn, block, &lds, &a.p, &per_launch);
-  hipEvent_t t0;
-  const bool timed = timing_begin(st, &t0);
-  rc = launch_groups(&a.p, fn, block, lds, &a, per_launch, st);
-  if (timed) timing_end(0, t0, st);
-  return rc;
+  return fwd_launch(p, wx, R, b, s0, states_out, carry_out, save, static_cast<char*>(ws),
+                    static_cast<uint32_t*>(ws), true, reinterpret_cast<hipStream_t>(stream));
 }
 
 int frnn_bwd(const frnn_desc* d, const void* R, const void* s0, const void* states, const void* save,
@@ -473,9 +500,9 @@ int frnn_bwd(const frnn_desc* d, const void* R, const void* s0, const void* stat
   const int tile = wide ? 64 : 32;
   const long long gwg = (long long)p.N * (p.GR * p.D / tile) * (p.D / tile) * p.splitk;
   timed = timing_begin(st, &t0);
-  const int h16 = p.mma == FRNN_MMA_BF16 ? FRNN_BF16 : (p.mma == FRNN_MMA_F16 ? FRNN_F16 : -1);
-  const bool dma = wide && h16 >= 0 && p.dt_io == h16 && p.dt_out == h16 &&
-                   (p.dt_state == h16 || p.dt_state == FRNN_F32) && !g_no_gemm_dma.load();
+  const int h16 = mma_h16(p.mma);
+  // fixed by the plan (the workspace was sized for it), not by the switch's current value
+  const bool dma = p.dma_gemm != 0;
   // FP32 -> MMA-type copy (rounded as the register-staged GEMM rounds its operands)
   auto to16 = [&](const float* src, unsigned short* dst, long n16) {
     int dt = h16;

@@ -59,8 +59,8 @@ struct GemmArgs {
 };
 
 // dR GEMM whose operand tiles are loaded by LDS-DMA several stages ahead: 16-bit
-// operands already in the MMA's type (dWx, states and s0 alike), D % 64 == 0, not
-// the GRU (whose candidate gate comes from an FP32 buffer); null otherwise.
+// operands in the MMA's type (dWx, states and s0 alike; the GRU's candidate gate
+// from its 16-bit copy dcand16), D % 64 == 0; null otherwise.
 const void* gemm_dma_kernel(int mma);
 // FP32 -> 16-bit copy (the DMA GEMM's h_{-1} rows when s0 is FP32).
 const void* to16_kernel();

@@ -18,7 +18,10 @@ state and the pointwise cell in FP32: the reference's
 ``dtype="float16"`` does the same with FP16 operands (FlashRNN2's FP16
 contract: FP16 inputs, FP32 compute and state). ``dtype="float32"`` runs the
 product in FP32 (the mathematical policy).
-Inputs may be BF16 or FP32 in either mode; outputs use the dtype of ``Wx``.
+Inputs may be BF16, FP16 or FP32 in either mode; the state history uses the
+dtype of ``Wx``. When ``Wx``, ``R`` and ``b`` differ in dtype, all three are
+promoted to FP32 for the call (``io_dtype``), so an FP32 ``R`` or ``b`` is
+never rounded to ``Wx``'s 16-bit type before the policy rounds the operands.
 
 ``last`` is the full-precision carry: it has the dtype of the ``states``
 argument (FP32 carries in give FP32 carries out), so chunked calls continue
@@ -232,6 +235,23 @@ def _check_shapes(cell, Wx, R, b, states):
         raise ValueError("flashrnn_amd runs on a ROCm GPU; inputs must be device tensors")
 
 
+def io_dtype(wx_dtype: torch.dtype, r_dtype: torch.dtype, b_dtype: torch.dtype) -> torch.dtype:
+    """The one tensor dtype the kernels run on when Wx, R and b differ.
+
+    The reference's config keeps separate ``dtype_w``, ``dtype_r`` and ``dtype_b``
+    (``flashrnn/flashrnn/flashrnn.py:187-264``, ``_get_config`` at ``:1096-1114``) and
+    compiles a kernel for that mix. Here all three are promoted to the widest of
+    them (FP32 if any is FP32; BF16 and FP16 together promote to FP32), so no
+    input loses precision before the policy rounds the recurrent operands; the
+    state history is returned in Wx's dtype and each gradient in its input's
+    dtype. Unsupported dtypes raise ``ValueError``."""
+    for name, dt in (("Wx", wx_dtype), ("R", r_dtype), ("b", b_dtype)):
+        if dt not in _IO:
+            raise ValueError(f"{name} dtype {dt} not supported; use bfloat16, float16 or float32")
+    kinds = {wx_dtype, r_dtype, b_dtype}
+    return kinds.pop() if len(kinds) == 1 else torch.float32
+
+
 def flashrnn(
     Wx: torch.Tensor,
     R: torch.Tensor,
@@ -247,9 +267,8 @@ def flashrnn(
         config = FlashRNNConfig(backend=backend, function=function, dtype=dtype)
     cell = config.function
     _check_shapes(cell, Wx, R, b, states)
-    io = Wx.dtype if Wx.dtype in _IO else torch.float32
-    if Wx.dtype not in _IO:
-        raise ValueError(f"Wx dtype {Wx.dtype} not supported; use bfloat16, float16 or float32")
+    out_dtype = Wx.dtype
+    io = io_dtype(Wx.dtype, R.dtype, b.dtype)
     mma = _MMA[config.dtype]
     B, T, _, N, D = Wx.shape
     S = CELL_SIZES[cell][3]
@@ -258,6 +277,7 @@ def flashrnn(
     else:
         st_dtype = states.dtype if states.dtype in _IO else io
         s0 = states.to(st_dtype)[:, :, 0]
+    Wx = Wx.to(io)
     R = R.to(io)
     b = b.to(io)
     # width: the kernels tile hidden units by 32; pad with inert units (zero
@@ -277,4 +297,4 @@ def flashrnn(
     if Dp != D:
         hist = hist[..., :D]
         carry = carry[..., :D]
-    return hist, carry.unsqueeze(2)
+    return hist.to(out_dtype), carry.unsqueeze(2)

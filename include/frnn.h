@@ -26,8 +26,15 @@
  *    the kernels run (a recurrence-exchange timeout, a workgroup placement
  *    that breaks the exchange protocol). frnn_status() reads it.
  *
- * Thread safety: stateless and reentrant. Calls that overlap in time must use
- * distinct workspaces.
+ * Thread safety: frnn_cell_sizes, frnn_workspace_bytes, frnn_fwd, frnn_bwd,
+ * frnn_status and frnn_strerror keep no state between calls and may run from
+ * several threads at once; calls that overlap in time must use distinct
+ * workspaces. The tuning, test and profiling setters (frnn_set_spin_limit,
+ * frnn_set_scouts, frnn_set_gemm_dma, frnn_timing_enable/_read,
+ * frnn_set_phase_profile) change process-global settings that every later
+ * call reads, on every thread: set them while no other thread is calling.
+ * frnn_set_gemm_dma also changes frnn_workspace_bytes(d, 1), so size the
+ * backward workspace after setting it.
  */
 #ifndef FRNN_H
 #define FRNN_H
@@ -193,7 +200,8 @@ void frnn_set_scouts(int enable);
 /* Tuning hook, no counterpart in the reference: enable (1, the default unless the
  * environment sets FRNN_NO_GEMM_DMA=1) or disable (0) the dR GEMM whose operand tiles
  * are loaded by LDS-DMA (used for 16-bit operands already in the MMA type and D % 64 == 0,
- * not the GRU). Both kernels give bitwise the same dR. */
+ * every cell; the GRU's FP32 candidate-gate cotangents and an FP32 s0 are first rounded
+ * to 16-bit copies in the backward workspace). Both kernels give bitwise the same dR. */
 void frnn_set_gemm_dma(int enable);
 
 #ifdef __cplusplus

@@ -28,7 +28,9 @@ import torch
 from oracle import numpy_explicit as ne
 from oracle.torch_restatement import SIZES, flashrnn_torch, recurrence
 
-GOLDEN = sorted(glob.glob(os.path.join(os.path.dirname(__file__), "golden", "*.npz")))
+GOLDEN = sorted(p for p in glob.glob(os.path.join(os.path.dirname(__file__), "golden", "*.npz"))
+                if not os.path.basename(p).startswith("c1_"))
+C1_FIXTURE = os.path.join(os.path.dirname(__file__), "golden", "c1_lstm_fp32.npz")
 
 
 def rand_inputs(cell, B=3, T=5, N=2, D=4, dtype=torch.float64, seed=20261005, scale=1.0):
@@ -145,6 +147,25 @@ def test_config1_lstm_fp32_forward_matches_library():
     out, (hT, cT) = m(wx[:, :, :, 0].reshape(4, 64, 256).double(), (s0[0, :, 0, 0][None].double(), s0[1, :, 0, 0][None].double()))
     torch.testing.assert_close(hist[0, :, :, 0].double(), out, atol=2e-5, rtol=0)
     torch.testing.assert_close(last[1, :, 0, 0].double(), cT[0], atol=2e-5, rtol=0)
+
+
+def test_config1_fixture():
+    """BASELINE config 1 exactly (B4 T64 N1 D64, FP32 inputs, seed 20261001): the oracle against
+    the committed torch.nn.LSTM fixture (tests/golden/make_c1.py), in FP64 to 1e-12 and in the
+    FP32 mathematical policy to 1e-5 max-abs-rel."""
+    z = np.load(C1_FIXTURE, allow_pickle=False)
+    args = [torch.from_numpy(z[k]) for k in ("wx", "R", "b", "s0")]
+    eh, el = torch.from_numpy(z["hist"]), torch.from_numpy(z["last"])
+    assert eh.shape == (2, 4, 64, 1, 64) and args[0].dtype == torch.float32
+    h64, l64 = flashrnn_torch(*(a.double() for a in args), cell="lstm")
+    torch.testing.assert_close(h64, eh, atol=1e-12, rtol=0)
+    torch.testing.assert_close(l64, el, atol=1e-12, rtol=0)
+    h32, l32 = flashrnn_torch(*args, cell="lstm", numerics="mathematical")
+    for a, e in ((h32, eh), (l32, el)):
+        assert ((a.double() - e).abs().max() / e.abs().max()).item() <= 1e-5
+    # the inputs are the ones config 1 names
+    g = torch.Generator().manual_seed(20261001)
+    torch.testing.assert_close(args[0], torch.randn(4, 64, 4, 1, 64, generator=g), atol=0, rtol=0)
 
 
 # --------------------------------------------------------------------- closed forms
