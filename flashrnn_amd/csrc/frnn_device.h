@@ -221,6 +221,10 @@ __device__ __forceinline__ Frag<MMA_F32> frag_rot8(const Frag<MMA_F32>& f) {
   return o;
 }
 template <int MMA>
+__device__ __forceinline__ Frag<MMA> frag_sel(bool c, const Frag<MMA>& a, const Frag<MMA>& b) {
+  return c ? a : b;
+}
+template <int MMA>
 __device__ __forceinline__ Frag<MMA> frag_keep(bool keep, const Frag<MMA>& f) {
   Frag<MMA> z;
   z.zero();

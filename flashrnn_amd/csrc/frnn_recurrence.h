@@ -370,6 +370,14 @@ __device__ __forceinline__ uint32_t gather_mma(const Xchg& x, const int (&word)[
 // half the loads; the odd tile then moves down 8 lanes (DPP) and the upper
 // lanes contribute zero. word[j] is the run of k-tile j for batch row lane % 8.
 // Long ranges are polled in chunks of PollChunk pairs, as in gather_mma.
+//
+// Split words (SPLIT) fill the padding columns instead: the even tile's
+// product takes hi in columns 0-7 and lo in columns 8-15 of one B operand, the
+// odd tile's likewise, so a pair costs two MFMAs, not four (one DPP rotation
+// trades the lower lanes' lo for the upper lanes' hi). Columns 0-7 of the
+// accumulators then hold the hi products and columns 8-15 the lo products of
+// the same batch rows; the caller adds column c + 8 into column c
+// (fold_cols8) before it reads them.
 template <int MMA, int NDT, int NF, bool SPLIT = false, bool SPEC = true, typename Zero, typename Prod,
           typename Between = NoWork>
 __device__ __forceinline__ uint32_t gather_pair_mma(const Xchg& x, const int (&word)[NF], bool bv, int off, int cstride, int nf,
@@ -385,13 +393,20 @@ __device__ __forceinline__ uint32_t gather_pair_mma(const Xchg& x, const int (&w
   const int hi = (threadIdx.x >> 3) & 1;  // lane % 16 >= 8
   // the pair's products: the even tile in place, the odd one moved down 8 lanes
   auto pair_prod = [&](Op o, int i) {
-    const Op odd = o.rot8();
-    o.keep(!hi);
-    o.apply([&](const Frag<MMA>& f, int part) { prod(0, 2 * i, f, part); });
-    if (2 * i + 1 < nf) {
-      Op od = odd;
-      od.keep(!hi);
-      od.apply([&](const Frag<MMA>& f, int part) { prod(0, 2 * i + 1, f, part); });
+    if constexpr (SPLIT) {
+      // lower lanes hold (hi, lo) of the even tile, upper lanes those of the odd tile
+      const Frag<MMA> got = frag_rot8(frag_sel<MMA>(hi, o.hi, o.lo));  // lower: hi_odd, upper: lo_even
+      prod(0, 2 * i, frag_sel<MMA>(hi, got, o.hi), 0);                   // [hi_even | lo_even]
+      if (2 * i + 1 < nf) prod(0, 2 * i + 1, frag_sel<MMA>(hi, o.lo, got), 0);  // [hi_odd | lo_odd]
+    } else {
+      const Op odd = o.rot8();
+      o.keep(!hi);
+      o.apply([&](const Frag<MMA>& f, int part) { prod(0, 2 * i, f, part); });
+      if (2 * i + 1 < nf) {
+        Op od = odd;
+        od.keep(!hi);
+        od.apply([&](const Frag<MMA>& f, int part) { prod(0, 2 * i + 1, f, part); });
+      }
     }
   };
   uint32_t spins = 0;
@@ -461,6 +476,19 @@ __device__ __forceinline__ uint32_t gather_pair_mma(const Xchg& x, const int (&w
     }
   }
   return spins;
+}
+
+// Accumulator lane l, register i holds column l % 16: add column c + 8 into
+// column c (lanes l and l ^ 8 of each 16-lane row; both get the sum).
+// (All four rotations read the unmodified accumulator and go through one
+// vector: an element-by-element read-modify-write of the accumulator was
+// compiled into rotations of the already-updated element 0 for elements 1-3.)
+__device__ __forceinline__ f32x4 fold_cols8(f32x4 v) {
+  typedef int i32x4 __attribute__((ext_vector_type(4)));
+  i32x4 r = __builtin_bit_cast(i32x4, v);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) r[i] = rot8(r[i]);
+  return v + __builtin_bit_cast(f32x4, r);
 }
 
 // ====================================================================== forward
@@ -1276,6 +1304,9 @@ __global__ void __launch_bounds__(64 * (KSC + 1) * NDT) bwd_kernel(BwdArgs a) {
     else
       polls = gather_mma<MMA, NDT, NB, NF, kSplit, kSpecB>(xc, xword, bval, xoff, cstride, nkt, ptag(p, it),
                                                            a.status, a.spin_limit, abort, zero, prod);
+    // paired split-word products: columns 8-15 hold the lo products of rows 0-7
+    if constexpr (kSplit && NB == 1)
+      if (pair && !cut) acc[0] = fold_cols8(acc[0]);
     prof.add(4, polls);
     prof.mark(0);
     prof.stamp(it, 2);
