@@ -21,6 +21,7 @@ FRNN_OUT_HIDDEN, FRNN_OUT_LAST, FRNN_SNAPSHOT_F32, FRNN_SLSTM_V1GRAD = 32, 64, 1
 FRNN_OK = 0
 FRNN_E_TIMEOUT = -5
 FRNN_E_PLACEMENT = -6
+FRNN_E_SCRATCH = -7
 
 CELLS = {"lstm": FRNN_LSTM, "gru": FRNN_GRU, "elman": FRNN_ELMAN, "slstm": FRNN_SLSTM}
 
@@ -46,6 +47,7 @@ EXPORTS = (
     "frnn_cell_sizes",
     "frnn_workspace_bytes",
     "frnn_fwd",
+    "frnn_fwd_noalloc",
     "frnn_bwd",
     "frnn_status",
     "frnn_strerror",
@@ -80,6 +82,8 @@ def load(path: str | os.PathLike | None = None) -> ctypes.CDLL:
     lib.frnn_workspace_bytes.restype = sz
     lib.frnn_fwd.argtypes = [dp, vp, vp, vp, vp, vp, vp, vp, vp, sz, vp]
     lib.frnn_fwd.restype = i32
+    lib.frnn_fwd_noalloc.argtypes = [dp, vp, vp, vp, vp, vp, vp, vp, vp, vp]
+    lib.frnn_fwd_noalloc.restype = i32
     lib.frnn_bwd.argtypes = [dp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, sz, vp]
     lib.frnn_bwd.restype = i32
     lib.frnn_status.argtypes = [vp, vp]

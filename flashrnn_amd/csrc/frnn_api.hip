@@ -404,6 +404,39 @@ int fwd_launch(const Plan& p, const void* wx, const void* R, const void* b, cons
   return rc;
 }
 
+// ---- scratch of the allocation-free forward (frnn_fwd_noalloc)
+// The forward workspace of a problem (status word aside: the caller passes it)
+// lives in this file-scope device array, one copy per GPU, held until the
+// process ends. Host code never passes the array's name to a kernel (on the
+// host it is only a stand-in for the symbol): it takes each device's address
+// once, with that device current, from hipGetSymbolAddress, and uses that.
+constexpr long long kScratchBytes = 8LL << 20;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+char* g_scratch_ptr[kMaxDevices] = {};
+
+int scratch_base(char** out) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) {
+    (void)hipGetLastError();
+    return FRNN_E_LAUNCH;
+  }
+  if (dev < 0 || dev >= kMaxDevices) return FRNN_E_UNSUPPORTED;
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* ptr = nullptr;
+    if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess || !ptr) {
+      (void)hipGetLastError();
+      return FRNN_E_LAUNCH;
+    }
+    g_scratch_ptr[dev] = static_cast<char*>(ptr);
+  }
+  *out = g_scratch_ptr[dev];
+  return FRNN_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -439,6 +472,19 @@ int frnn_fwd(const frnn_desc* d, const void* wx, const void* R, const void* b, c
   if ((long long)ws_bytes < p.ws_fwd) return FRNN_E_WORKSPACE;
   return fwd_launch(p, wx, R, b, s0, states_out, carry_out, save, static_cast<char*>(ws),
                     static_cast<uint32_t*>(ws), true, reinterpret_cast<hipStream_t>(stream));
+}
+
+int frnn_fwd_noalloc(const frnn_desc* d, const void* wx, const void* R, const void* b, const void* s0,
+                     void* states_out, void* carry_out, void* save, void* status, frnn_stream_t stream) {
+  Plan p;
+  int rc = make_plan(d, &p);
+  if (rc != FRNN_OK) return rc;
+  if (!status) return FRNN_E_INVALID;
+  if (p.ws_fwd > kScratchBytes) return FRNN_E_SCRATCH;
+  char* base = nullptr;
+  if ((rc = scratch_base(&base)) != FRNN_OK) return rc;
+  return fwd_launch(p, wx, R, b, s0, states_out, carry_out, save, base, static_cast<uint32_t*>(status), false,
+                    reinterpret_cast<hipStream_t>(stream));
 }
 
 int frnn_bwd(const frnn_desc* d, const void* R, const void* s0, const void* states, const void* save,
@@ -550,6 +596,8 @@ const char* frnn_strerror(int code) {
     case FRNN_E_LAUNCH: return "HIP kernel launch failed (co-residency or resources)";
     case FRNN_E_TIMEOUT: return "recurrence exchange timed out on the device";
     case FRNN_E_PLACEMENT: return "an XCD received more workgroups than its slots; retry with FRNN_XCD_SHARED";
+    case FRNN_E_SCRATCH:
+      return "frnn_fwd_noalloc: the problem's forward workspace exceeds the static scratch (8 MiB); use frnn_fwd";
   }
   return "unknown frnn error";
 }

@@ -126,6 +126,7 @@ enum frnn_status {
   FRNN_E_LAUNCH = -4,      /* the HIP runtime refused a launch (co-residency, resources) */
   FRNN_E_TIMEOUT = -5,     /* device: a recurrence exchange did not arrive within the spin limit */
   FRNN_E_PLACEMENT = -6,   /* device: an XCD received more workgroups than it has slots */
+  FRNN_E_SCRATCH = -7,     /* frnn_fwd_noalloc: the forward workspace exceeds its static scratch */
 };
 
 /* Gate and state counts of a cell: (G_R, G_W, G_T, S); flashrnn/flashrnn/flashrnn.py:45-70. */
@@ -144,6 +145,24 @@ size_t frnn_workspace_bytes(const frnn_desc* d, int which);
 int frnn_fwd(const frnn_desc* d, const void* wx, const void* R, const void* b, const void* s0,
              void* states_out, void* carry_out, void* save, void* ws, size_t ws_bytes,
              frnn_stream_t stream);
+
+/* Allocation-free forward. No counterpart in the reference: it is for callers that
+ * cannot allocate device memory, or have a library do so, around the call -- code under
+ * HIP graph capture, tight serving loops, harnesses that forbid it.
+ * Same arguments, results and kernels as frnn_fwd, except that the forward workspace
+ * (exchange tables and workgroup slot counters) lives in a static device array of the
+ * library, 8 MiB per GPU, held by each GPU it runs on until the process ends; the call
+ * makes no hipMalloc, hipFree or allocating library call. status: a caller-owned device
+ * word (4 bytes, zeroed once by the caller) that receives the sticky device status, as
+ * the first word of frnn_fwd's workspace does (frnn_status(status, stream) reads it).
+ * Returns FRNN_E_SCRATCH when frnn_workspace_bytes(d, 0) exceeds 8 MiB (about
+ * groups * D <= 32768 with 16-bit operands, 16384 with FP32, groups = N * ceil(B/16)).
+ * Every call on one GPU shares that GPU's array, and the array keeps the last call's
+ * contents (each call clears what must start at zero): calls that overlap in time on
+ * one GPU race -- serialise them on one stream. save is the caller's area, as in
+ * frnn_fwd (may be NULL unless FRNN_TRAINING). */
+int frnn_fwd_noalloc(const frnn_desc* d, const void* wx, const void* R, const void* b, const void* s0,
+                     void* states_out, void* carry_out, void* save, void* status, frnn_stream_t stream);
 
 /* Backward. Replaces FlashRNNFuncFused::backward (fused/flashrnn.cc:335-435).
  * R, s0, states (the forward's states_out) and save must be those of the
