@@ -136,41 +136,54 @@ def _time_ms(torch, fn, reps=20, warmup=3):
     return round(times[len(times) // 2], 4)
 
 
+# The reference's published head-dimension sweep (v1 cuda_fused LSTM, B16 T1024 bf16, H100 SXM;
+# README speed figure head_dim--lstm.svg, harness speed_experiments/kernel_speed_benchmark.py:104-128):
+# (DH, NH): (forward ms, forward+backward ms)
+REFERENCE_SWEEP = {(16, 48): (3.56, 8.22), (32, 24): (2.9, 8.2), (64, 12): (3.1, 8.64), (128, 6): (3.22, 9.02),
+                   (256, 3): (3.62, 11.3), (768, 1): (4.87, 13.61)}
+
+
+def head_dim_sweep(torch, dev, flashrnn):
+    """Forward and forward+backward time of the LSTM at every point of the reference's published
+    head-dimension sweep (B16 T1024, NH*DH = 768, bf16), beside the H100 cuda_fused figures."""
+    out = []
+    Bp = 16
+    for (dh_, nh_), (ref_f, ref_fb) in REFERENCE_SWEEP.items():
+        g = torch.Generator().manual_seed(7)
+        wx = torch.randn(Bp, T, G, nh_, dh_, generator=g).to(dev, torch.bfloat16).requires_grad_()
+        R = (torch.randn(G, nh_, dh_, dh_, generator=g) / dh_**0.5).to(dev, torch.bfloat16).requires_grad_()
+        b = (0.1 * torch.randn(G, nh_, dh_, generator=g)).to(dev, torch.bfloat16).requires_grad_()
+        s0 = torch.zeros(S, Bp, 1, nh_, dh_, device=dev, dtype=torch.bfloat16, requires_grad=True)
+        dh = torch.randn(S, Bp, T, nh_, dh_, generator=g).to(dev, torch.bfloat16)
+        dl = torch.randn(S, Bp, 1, nh_, dh_, generator=g).to(dev, torch.bfloat16)
+
+        def fwd():
+            with torch.no_grad():
+                flashrnn(wx, R, b, s0, function="lstm", dtype="bfloat16")
+
+        def fwdbwd():
+            h, last = flashrnn(wx, R, b, s0, function="lstm", dtype="bfloat16")
+            torch.autograd.grad((h, last), (wx, R, b, s0), grad_outputs=(dh, dl))
+
+        f_ms, fb_ms = _time_ms(torch, fwd), _time_ms(torch, fwdbwd)
+        out.append({"DH": dh_, "NH": nh_, "fwd_ms": f_ms, "fwd_bwd_ms": fb_ms,
+                    "h100_cuda_fused_fwd_ms": ref_f, "h100_cuda_fused_fwd_bwd_ms": ref_fb,
+                    "ratio_fwd": round(ref_f / f_ms, 2), "ratio_fwd_bwd": round(ref_fb / fb_ms, 2)})
+    return out
+
+
 def extras(torch, dev, flashrnn):
     """Side measurements, not the metric:
-    * the shape of the reference's only published timing of this path (v1
-      cuda_fused LSTM, B16 T1024 N3 D256 bf16, H100 SXM: forward 3.62 ms,
-      forward+backward 11.3 ms; README speed figure head_dim--lstm.svg);
+    * the reference's published head-dimension sweep (v1 cuda_fused LSTM,
+      B16 T1024 bf16, H100 SXM; README speed figure head_dim--lstm.svg),
+      every (DH, NH) point, forward and forward+backward;
     * FlashRNN2's prepared inference (forward only, hidden-state output,
       captured HIP graph) at the metric's shape B8 T1024 N3 D256.
     Inputs are seeded normals as in make_inputs."""
     from flashrnn_amd.prepared import PreparedSequence
 
-    out = {}
+    out = {"reference_published_sweep": head_dim_sweep(torch, dev, flashrnn)}
     g = torch.Generator().manual_seed(7)
-    Bp = 16
-    wx = torch.randn(Bp, T, G, N, D, generator=g).to(dev, torch.bfloat16).requires_grad_()
-    R = (torch.randn(G, N, D, D, generator=g) / D**0.5).to(dev, torch.bfloat16).requires_grad_()
-    b = (0.1 * torch.randn(G, N, D, generator=g)).to(dev, torch.bfloat16).requires_grad_()
-    s0 = torch.zeros(S, Bp, 1, N, D, device=dev, dtype=torch.bfloat16, requires_grad=True)
-    dh = torch.randn(S, Bp, T, N, D, generator=g).to(dev, torch.bfloat16)
-    dl = torch.randn(S, Bp, 1, N, D, generator=g).to(dev, torch.bfloat16)
-
-    def fwd():
-        with torch.no_grad():
-            flashrnn(wx, R, b, s0, function="lstm", dtype="bfloat16")
-
-    def fwdbwd():
-        h, last = flashrnn(wx, R, b, s0, function="lstm", dtype="bfloat16")
-        torch.autograd.grad((h, last), (wx, R, b, s0), grad_outputs=(dh, dl))
-
-    f_ms, fb_ms = _time_ms(torch, fwd), _time_ms(torch, fwdbwd)
-    out["reference_published_shape"] = {
-        "workload": "LSTM B16 T1024 N3 D256 bf16",
-        "fwd_ms": f_ms, "fwd_bwd_ms": fb_ms,
-        "h100_cuda_fused_fwd_ms": 3.62, "h100_cuda_fused_fwd_bwd_ms": 11.3,
-        "speedup_fwd": round(3.62 / f_ms, 2), "speedup_fwd_bwd": round(11.3 / fb_ms, 2),
-    }
     x = torch.randn(B, T, G, N, D, generator=g).to(dev, torch.bfloat16)
     Rp = (torch.randn(G, N, D, D, generator=g) / D**0.5).to(dev, torch.bfloat16)
     bp = (0.1 * torch.randn(G, N, D, generator=g)).to(dev, torch.bfloat16)
@@ -334,6 +347,22 @@ def main(argv=None):
             "traffic_source": os.path.relpath(TRAFFIC_FILE, os.path.dirname(os.path.abspath(__file__))),
         },
     }
+    # HBM rates of the recurrences' streams: the algorithmic bytes of the Wx / state
+    # streams (16-bit tensors) and the measured traffic of the committed rocprof
+    # summary, over each kernel's average duration in this run
+    stream_bytes = {
+        "forward recurrence": {"Wx read": B * T * G * N * D * 2, "states written": S * B * T * N * D * 2},
+        "backward recurrence": {"d_states read": S * B * T * N * D * 2, "dWx written": B * T * G * N * D * 2},
+    }
+    hbm = {}
+    for k, (name, tag) in enumerate(zip(names[:2], KERNEL_TAGS[:2])):
+        alg = sum(stream_bytes[name].values())
+        meas = measured_traffic(tag)
+        hbm[name] = {"stream_bytes": stream_bytes[name], "stream_GBps": round(alg / (avg[k] / 1e3) / 1e9, 1),
+                     "measured_traffic_bytes": meas,
+                     "measured_GBps": round(meas / (avg[k] / 1e3) / 1e9, 1) if meas else None,
+                     "peak_GBps": 8000.0}
+    result["hbm"] = hbm
     if args.phases:
         prof = torch.zeros(256 + 2 * 128 * 16 * 64, dtype=torch.int64, device=dev)
         lib.frnn_set_phase_profile(prof.data_ptr())

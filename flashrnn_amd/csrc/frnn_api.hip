@@ -182,6 +182,12 @@ int make_plan(const frnn_desc* d, Plan* p) {
   p->t0 = d->step_base;
   if (p->t0 < 0 || p->Ttot < 1 || (long long)p->t0 + d->steps > p->Ttot) return FRNN_E_INVALID;
   p->dt_out = (d->flags & FRNN_SNAPSHOT_F32) ? FRNN_F32 : d->dtype_io;
+  // saved-for-backward values: FP16 under the 16-bit operand policies (every value
+  // the LSTM, GRU and Elman save is an activation in [-1, 1], a state or a gate
+  // pre-activation, |x| < 65504; FP16 keeps 11 significant bits), FP32 with FP32
+  // operands (1e-4 parity) and for the sLSTM (its gradient is ill-conditioned at a
+  // zero start, and its normalizer state grows with the sequence)
+  p->dt_save = (d->mma != FRNN_MMA_F32 && d->cell != FRNN_SLSTM) ? FRNN_F16 : FRNN_F32;
   // the backward needs the hidden-state history of the whole sequence (its dR GEMM operand)
   if ((d->flags & FRNN_TRAINING) && ((d->flags & FRNN_OUT_LAST) || p->Ttot != d->steps)) return FRNN_E_UNSUPPORTED;
   if (d->flags & FRNN_GRAD_CLIP) {
@@ -197,6 +203,10 @@ int make_plan(const frnn_desc* d, Plan* p) {
   const int KT = p->kt_fwd;
   // hidden tiles per workgroup: a group must fit the 32 CUs of one XCD
   p->NDT = (p->D / 16 <= 32) ? 1 : 2;
+  // FRNN_NDT=2 (environment, read per plan): two hidden tiles per workgroup at any
+  // width with an even tile count (half the workgroups per group)
+  if (const char* e = std::getenv("FRNN_NDT"))
+    if (std::atoi(e) == 2 && (p->D / 16) % 2 == 0) p->NDT = 2;
   // contraction split (compute waves per hidden tile, plus one I/O wave): forward
   // up to 4; backward up to 8 where D/32 >= 8 (its exchange operand is GR times
   // wider, so splitting it further shortens each wave's poll). Two-tile
@@ -238,7 +248,7 @@ int make_plan(const frnn_desc* d, Plan* p) {
   split = std::min<long long>(split, std::max<long long>(1, ktt / 8));
   p->splitk = (int)std::min<long long>(split, 64);
   // saved-for-backward area: the lane-native values only
-  p->save_bytes = align_up(p->save_floats * 4);
+  p->save_bytes = align_up(p->save_floats * (p->dt_save == FRNN_F32 ? 4 : 2));
   // workspaces: status word at 0, exchange at 256
   p->off_x = kAlign;
   // by a launch's first group: the members' counters, then the scouts'
@@ -384,7 +394,7 @@ int fwd_launch(const Plan& p, const void* wx, const void* R, const void* b, cons
   a.s0 = s0;
   a.states = states_out;
   a.carry = carry_out;
-  a.save = training ? static_cast<float*>(save) : nullptr;
+  a.save = training ? save : nullptr;
   a.xbuf = w + p.off_x;
   a.xbytes = xbytes;
   a.claim = reinterpret_cast<uint32_t*>(w + p.off_claim_f);
@@ -506,7 +516,7 @@ int frnn_bwd(const frnn_desc* d, const void* R, const void* s0, const void* stat
   frnn::BwdArgs a;
   a.p = p;
   a.R = R;
-  a.save = static_cast<const float*>(save);
+  a.save = save;
   a.d_states = d_states;
   a.d_carry = d_carry;
   a.dwx = dwx;

@@ -104,6 +104,42 @@ __device__ __forceinline__ void st4(void* p, long i, int dt, f32x4 v) {
   }
 }
 
+// Four consecutive values of SZ bytes each, with the element size fixed at
+// compile time (SZ = 4: FP32; SZ = 2: BF16, or FP16 when f16): loads move raw
+// bits and conversions are branch-free selects, so no load waits at a dtype
+// branch (a value merged from two branches is "used" at the merge, which
+// makes the compiler wait for the load there).
+template <int SZ>
+__device__ __forceinline__ u32x4 ld4s(const void* p, long i) {
+  if constexpr (SZ == 4) {
+    return *reinterpret_cast<const u32x4*>(static_cast<const float*>(p) + i);
+  } else {
+    const uint2 u = *reinterpret_cast<const uint2*>(static_cast<const unsigned short*>(p) + i);
+    return u32x4{u.x, u.y, 0u, 0u};
+  }
+}
+template <int SZ>
+__device__ __forceinline__ f32x4 cvt4s(u32x4 r, bool f16) {
+  if constexpr (SZ == 4) {
+    return __builtin_bit_cast(f32x4, r);
+  } else {
+    const f32x4 b = {u2f(r[0] << 16), u2f(r[0] & 0xffff0000u), u2f(r[1] << 16), u2f(r[1] & 0xffff0000u)};
+    const f32x4 h = {f16_to_f32(r[0] & 0xffffu), f16_to_f32(r[0] >> 16), f16_to_f32(r[1] & 0xffffu),
+                     f16_to_f32(r[1] >> 16)};
+    return f16 ? h : b;
+  }
+}
+template <int SZ>
+__device__ __forceinline__ void st4s(void* p, long i, f32x4 v, bool f16) {
+  if constexpr (SZ == 4) {
+    *reinterpret_cast<f32x4*>(static_cast<float*>(p) + i) = v;
+  } else {
+    const uint2 b = {bf16_bits(v[0]) | (bf16_bits(v[1]) << 16), bf16_bits(v[2]) | (bf16_bits(v[3]) << 16)};
+    const uint2 h = {f16_bits(v[0]) | (f16_bits(v[1]) << 16), f16_bits(v[2]) | (f16_bits(v[3]) << 16)};
+    *reinterpret_cast<uint2*>(static_cast<unsigned short*>(p) + i) = f16 ? h : b;
+  }
+}
+
 // Activations from the hardware exp2 / log2 / reciprocal (v_exp_f32,
 // v_log_f32, v_rcp_f32); formulas are the textbook ones.
 __device__ __forceinline__ float fexp(float x) { return __builtin_amdgcn_exp2f(x * 1.4426950408889634f); }

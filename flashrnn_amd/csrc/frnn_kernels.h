@@ -15,7 +15,7 @@ struct FwdArgs {
   const void* s0;
   void* states;
   void* carry;
-  float* save;              // lane-native saved values (training) or null
+  void* save;               // lane-native saved values (training, dtype p.dt_save) or null
   char* xbuf;               // exchange, both parities
   long long xbytes;
   uint32_t* claim;          // zeroed slot counters (XCD-local exchange)
@@ -27,7 +27,7 @@ struct FwdArgs {
 struct BwdArgs {
   Plan p;
   const void* R;
-  const float* save;
+  const void* save;         // lane-native saved values (dtype p.dt_save)
   const void* d_states;     // may be null
   const void* d_carry;      // may be null
   void* dwx;

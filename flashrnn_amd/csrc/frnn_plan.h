@@ -32,6 +32,8 @@ struct Plan {
   int Ttot, t0;    // forward step window: Wx and the outputs hold Ttot steps, this call runs
                    // steps [t0, t0 + T) of them (Ttot == T, t0 == 0 for a whole sequence)
   int dt_out;      // dtype of the state output (dt_io, or FP32 with kFlagSnapF32)
+  int dt_save;     // dtype of the saved-for-backward values: FP16 with 16-bit MMA operands
+                   // (LSTM, GRU, Elman), FP32 otherwise
   int NB;          // 16-row batch tiles per group
   int BS;          // slab rows = 16 * NB
   int nslab;       // ceil(B / BS)

@@ -34,10 +34,12 @@ constexpr int kFwdRing = 2;   // raw Wx slots in LDS (DMA targets)
 constexpr int kFwdXf = 3;     // converted (FP32) Wx slots in LDS (what the owners read)
 constexpr int kFwdAhead = 3;  // steps a Wx load goes out ahead of its use
 
-template <int CELL>
-struct BwdRing {  // input steps staged ahead, bounded by the I/O wave's registers
-  static constexpr int P = 2;
-};
+// Backward input pipeline: the I/O wave keeps kBwdRegs iterations of loads in
+// flight in registers and stages inputs into kBwdStage LDS slots, two
+// iterations ahead of their use, so the owners can read an iteration's inputs
+// during the previous iteration's poll.
+constexpr int kBwdRegs = 2;
+constexpr int kBwdStage = 3;
 
 // LDS layout of a team:
 //   forward : red  [2][KS][NB][272 slots][4 gates]        MFMA partial sums; slot
@@ -47,21 +49,23 @@ struct BwdRing {  // input steps staged ahead, bounded by the I/O wave's registe
 //             xring[slot][gate][64 chunks][16 bytes]       raw Wx of the next steps
 //                  (chunk = row * 4 + quad: FP32 units 4*quad..+3; BF16 units
 //                   4*quad..+7 in the even quads, odd quads unused)
-//             ost  [2][value][NE]                         states + saved values,
+//             ost  [2][value][NE]                         states + saved values (FP32),
 //                  value-major so the drain reads 4 elements per 16-byte read
 //             xf   [slot][gate][NE]                       Wx of a step in FP32,
 //                  converted from the raw slot by the I/O wave
 //   backward: red  [2][NB][KS][304]                       partial R^T dG at
 //                  red_idx(lane*4 + reg): 16 spare floats per 64, so the
 //                  16-byte writes and the owners' scalar reads are conflict-free
-//             iring[P][NE][NOP]                           state cotangents + saved values
-//             ost  [2][NE][4]                             dWx (+ GRU candidate cotangent)
+//             iring[3][S + NSAVE][NE]                     state cotangents + saved values,
+//                  value-major: the I/O wave writes four elements of a value
+//                  per 16-byte write (lane-contiguous, no bank conflicts)
+//             ost  [2][4][NE]                             dWx (+ GRU candidate cotangent),
+//                  value-major likewise
 template <int CELL, int NB>
 struct Lds {
   static constexpr int NE = NB * 256;
   static constexpr int GR = CellShape<CELL>::GR, GW = CellShape<CELL>::GW, S = CellShape<CELL>::S;
   static constexpr int NSAVE = Cell<CELL>::NSAVE;
-  static constexpr int NOP = (S + NSAVE + 3) / 4 * 4;        // per-element staged values, padded
   static constexpr int NOB = 4;                              // backward outputs per element, padded
   // floats per team
   static constexpr int NV = S + NSAVE;                      // staged values per element (forward)
@@ -73,7 +77,7 @@ struct Lds {
     return 2L * KS * NB * RED_F + (long)kFwdRing * RING + 2L * NV * NE + (long)kFwdXf * XF;
   }
   __host__ __device__ static constexpr long bwd(int KS) {
-    return 2L * NB * KS * RED_B + (long)BwdRing<CELL>::P * NE * NOP + 2L * NE * NOB;
+    return 2L * NB * KS * RED_B + (long)kBwdStage * NE * NV + 2L * NE * NOB;
   }
 };
 
@@ -491,6 +495,18 @@ __device__ __forceinline__ f32x4 fold_cols8(f32x4 v) {
   return v + __builtin_bit_cast(f32x4, r);
 }
 
+// Element-size class of an I/O wave: 0 = 16-bit tensors and states, 1 = 16-bit
+// tensors (Wx, dWx) with FP32 states (snapshot), 2 = FP32 tensors and states.
+__host__ __device__ __forceinline__ int io_sizes(int dt_io, int dt_out) {
+  return dt_io == DT_F32 ? 2 : (dt_out == DT_F32 ? 1 : 0);
+}
+// Bytes of a saved-for-backward value: FP16 under the 16-bit operand policies
+// (LSTM, GRU, Elman), FP32 for FP32 operands and for the sLSTM (the host plan's
+// dt_save says the same).
+template <int CELL, int MMA> struct SaveSize {
+  static constexpr int value = (MMA != MMA_F32 && CELL != CELL_SLSTM) ? 2 : 4;
+};
+
 // ====================================================================== forward
 // I/O lane l serves the elements e = 256*(i/4) + 4*l + i%4: four consecutive
 // hidden units of one batch row, so every global access is one 8/16-byte
@@ -501,12 +517,19 @@ __device__ __forceinline__ int io_elem(int lane, int i) { return 256 * (i >> 2) 
 // I/O wave of a team. Wx of step u is loaded straight into raw slot u % 2 by
 // LDS-DMA (global_load_lds: no registers in flight), three steps ahead; two
 // steps ahead of its use the wave converts it to FP32 in slot u % 3 of the
-// area the owners read (so the runtime dtype is off their critical path). After barrier t it also drains step t-1's
-// outputs from the staging area. Per step the wave issues the same loads and
-// stores in the same order, so the count of operations issued after a step's
-// loads is a constant in the steady state. Padding batch rows are neither
-// loaded nor stored (their converted values are never used).
-template <int CELL, int MMA, int NB>
+// area the owners read (so the runtime dtype is off their critical path).
+// After barrier t it also drains step t-1's outputs from the staging area.
+// Per step the wave issues the same loads and stores in the same order, so the
+// count of operations issued after a step's loads is a constant in the steady
+// state. Padding batch rows are neither loaded nor stored (their converted
+// values are never used).
+//
+// XS, OS, SS: element sizes (2 or 4 bytes) of Wx, of the state output and of
+// the saved values, fixed at compile time; BF16 vs FP16 is a branch-free
+// select. This wave sits close to the step's critical path: each of its LDS
+// bursts (all reads, then all writes or stores) issues without waiting
+// between the accesses.
+template <int CELL, int MMA, int NB, int XS, int OS, int SS>
 __device__ void fwd_io(const FwdArgs& a, const Team& tm, float* xring, float* ost, float* xf) {
   static_assert(NB == 1, "one 16-row batch tile per group");
   using CS = CellShape<CELL>;
@@ -515,44 +538,52 @@ __device__ void fwd_io(const FwdArgs& a, const Team& tm, float* xring, float* os
   const Plan& p = a.p;
   const int T = p.T, N = p.N, D = p.D, B = p.B, TT = p.Ttot, t0 = p.t0;
   const bool training = (p.flags & 1) != 0;
+  const bool xf16 = p.dt_io == DT_F16, of16 = p.dt_out == DT_F16, sf16 = p.dt_save == DT_F16;
   // output policy: all S states, the hidden state only, or the sequence's last hidden state only
   const int mode = (p.flags & kFlagOutLast) ? 2 : ((p.flags & kFlagOutHidden) ? 1 : 0);
   const int nst = mode == 0 ? S : 1;
   const long wx_t = (long)GW * N * D;
-  // loads: lane -> (row, quad); BF16 chunks hold 8 units, so odd quads idle
+  // loads: lane -> (row, quad); 16-bit chunks hold 8 units, so odd quads idle
   const int lrow = tm.lane >> 2, lquad = tm.lane & 3;
   const int lb = tm.slab * p.BS + lrow;
-  const bool lval = lb < B && (p.dt_io == DT_F32 || (lquad & 1) == 0);
+  const bool lval = lb < B && (XS == 4 || (lquad & 1) == 0);
   const long lbase = ((long)lb * TT + t0) * wx_t + (long)tm.n * D + tm.dt * 16 + 4 * lquad;
-  const int esz = p.dt_io == DT_F32 ? 4 : 2;
   auto load_wx = [&](int u) {
     float* slot = xring + (long)(u % kFwdRing) * RING;
 #pragma unroll
     for (int g = 0; g < GW; ++g) {
-      const char* src = static_cast<const char*>(a.wx) + (lbase + (long)u * wx_t + (long)g * N * D) * esz;
+      const char* src = static_cast<const char*>(a.wx) + (lbase + (long)u * wx_t + (long)g * N * D) * XS;
       if (lval)
         __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)(slot + g * 256), 16, 0, 0);
     }
   };
-  // stores: lane -> elements e0 .. e0+3 (four units of one row)
+  // stores: lane -> elements e0 .. e0+3 (four units of one row), from base
+  // offsets that advance by a constant per step
   const int e0 = io_elem(tm.lane, 0);
   const Elem el = elem_of(p, tm, e0);
+  long st_off[S];
+#pragma unroll
+  for (int k = 0; k < S; ++k) st_off[k] = ((((long)k * B + el.b) * TT + t0) * N + tm.n) * D + el.d;
+  const long st_step = (long)N * D;
+  const long sv_off = save_index(p, NE, 0, tm.wgi, 0, tm.team, e0);
+  const long sv_per = (long)p.NDT * NE, sv_step = (long)p.nwg * p.nsave * sv_per;
   auto store_out = [&](int t, const float* src) {
     if (mode == 2) {  // [B,1,N,D]: the last step of the sequence only
       if (t0 + t == TT - 1 && el.real)
-        st4(a.states, ((long)el.b * N + tm.n) * D + el.d, p.dt_out, *reinterpret_cast<const f32x4*>(src + e0));
+        st4s<OS>(a.states, ((long)el.b * N + tm.n) * D + el.d, *reinterpret_cast<const f32x4*>(src + e0), of16);
       return;
     }
+    // every staged value is read (unused ones too), so the reads form one burst
+    f32x4 x[NV];
+#pragma unroll
+    for (int v = 0; v < NV; ++v) x[v] = *reinterpret_cast<const f32x4*>(src + v * NE + e0);
+    if (!el.real) return;
 #pragma unroll
     for (int v = 0; v < NV; ++v) {
       if (v >= S && !training) break;
       if (v < S && v >= nst) continue;  // the policy's states only: [nst,B,T,N,D]
-      const f32x4 x = *reinterpret_cast<const f32x4*>(src + v * NE + e0);
-      if (!el.real) continue;
-      if (v < S)
-        st4(a.states, ((((long)v * B + el.b) * TT + t0 + t) * N + tm.n) * D + el.d, p.dt_out, x);
-      else
-        *reinterpret_cast<f32x4*>(a.save + save_index(p, NE, t, tm.wgi, v - S, tm.team, e0)) = x;
+      if (v < S) st4s<OS>(a.states, st_off[v] + t * st_step, x[v], of16);
+      else st4s<SS>(a.save, sv_off + (v - S) * sv_per + t * sv_step, x[v], sf16);
     }
   };
 
@@ -564,18 +595,19 @@ __device__ void fwd_io(const FwdArgs& a, const Team& tm, float* xring, float* os
   auto convert = [&](int u) {
     const float* slot = xring + (long)(u % kFwdRing) * RING;
     float* dst = xf + (long)(u % kFwdXf) * Lds<CELL, NB>::XF;
+    u32x4 raw[GW];
 #pragma unroll
     for (int g = 0; g < GW; ++g) {
-      f32x4 x;
-      if (p.dt_io == DT_F32) {
-        x = *reinterpret_cast<const f32x4*>(slot + g * 256 + (lrow * 4 + lquad) * 4);
+      if constexpr (XS == 4) {
+        raw[g] = *reinterpret_cast<const u32x4*>(slot + g * 256 + (lrow * 4 + lquad) * 4);
       } else {
         const uint2 h = *reinterpret_cast<const uint2*>(reinterpret_cast<const char*>(slot + g * 256) +
                                                         (lrow * 4 + (lquad >> 1) * 2) * 16 + (lquad & 1) * 8);
-        x = raw4_f32(u32x4{h.x, h.y, 0u, 0u}, p.dt_io);
+        raw[g] = u32x4{h.x, h.y, 0u, 0u};
       }
-      *reinterpret_cast<f32x4*>(dst + g * NE + e0) = x;
     }
+#pragma unroll
+    for (int g = 0; g < GW; ++g) *reinterpret_cast<f32x4*>(dst + g * NE + e0) = cvt4s<XS>(raw[g], xf16);
   };
   // Per iteration t: barrier t; convert step t+2 (its loads went out in
   // iteration t-1; the owners read it after barrier t+1); issue the loads of
@@ -708,7 +740,13 @@ __global__ void __launch_bounds__(64 * (KSC + 1) * NDT) fwd_kernel(FwdArgs a) {
     }
   }
   if (tm.kw == KS) {
-    fwd_io<CELL, MMA, NB>(a, tm, xring, ost, xf);
+    // saved values: FP16 under the 16-bit policies (sLSTM: FP32), FP32 with FP32 operands
+    constexpr int SS = SaveSize<CELL, MMA>::value;
+    switch (io_sizes(p.dt_io, p.dt_out)) {
+      case 0: fwd_io<CELL, MMA, NB, 2, 2, SS>(a, tm, xring, ost, xf); break;
+      case 1: fwd_io<CELL, MMA, NB, 2, 4, SS>(a, tm, xring, ost, xf); break;
+      default: fwd_io<CELL, MMA, NB, 4, 4, SS>(a, tm, xring, ost, xf); break;
+    }
     return;
   }
 
@@ -922,102 +960,90 @@ __global__ void __launch_bounds__(64 * (KSC + 1) * NDT) fwd_kernel(FwdArgs a) {
 }
 
 // ===================================================================== backward
-// I/O wave of a team: inputs (state cotangents, saved values) of iteration
-// it+1 into the ring before barrier `it`; outputs of iteration `it` after it.
-template <int CELL, int MMA, int NB>
+// I/O wave of a team. Per iteration it (step t = T-1-it), before barrier it:
+// stage the inputs of iteration it+2 (state cotangents and saved values,
+// converted to FP32) from registers into LDS slot (it+2) % 3, then issue the
+// loads of iteration it+4 into the registers just freed; after barrier it:
+// drain iteration it's outputs (dWx, GRU: candidate cotangents). Every LDS
+// access is lane-contiguous (value-major layouts). XS, OS, SS: element sizes
+// (2 or 4 bytes) of dWx, of the state cotangents and of the saved values,
+// fixed at compile time (see fwd_io).
+template <int CELL, int MMA, int NB, int XS, int OS, int SS>
 __device__ void bwd_io(const BwdArgs& a, const Team& tm, float* iring, float* ost) {
+  static_assert(NB == 1, "one 16-row batch tile per group");
   using CS = CellShape<CELL>;
-  constexpr int GW = CS::GW, S = CS::S, NE = NB * 256, IOQ = NB, P = BwdRing<CELL>::P;
-  constexpr int NSAVE = Cell<CELL>::NSAVE, NIN = S + NSAVE, NOP = Lds<CELL, NB>::NOP, NOB = Lds<CELL, NB>::NOB;
+  constexpr int GW = CS::GW, S = CS::S, NE = NB * 256, PR = kBwdRegs;
+  constexpr int NSAVE = Cell<CELL>::NSAVE, NIN = S + NSAVE, NOB = Lds<CELL, NB>::NOB;
   const Plan& p = a.p;
   const int T = p.T, N = p.N, D = p.D, B = p.B;
-  const long wx_t = (long)GW * N * D;
+  const bool xf16 = p.dt_io == DT_F16, of16 = p.dt_out == DT_F16, sf16 = p.dt_save == DT_F16;
   const bool hidden_only = (p.flags & kFlagOutHidden) != 0;  // d_states [B,T,N,D]: the hidden state's only
-  Elem el[IOQ];
-  int e0[IOQ];
+  const int e0 = io_elem(tm.lane, 0);
+  const Elem el = elem_of(p, tm, e0);
+  // per-lane element offsets at step 0, and their step strides
+  const long ds_off = (((long)el.b * T) * N + tm.n) * D + el.d;  // + k * B*T*N*D + t * N*D
+  const long ds_k = (long)B * T * N * D, ds_t = (long)N * D;
+  const long sv_off = save_index(p, NE, 0, tm.wgi, 0, tm.team, e0);
+  const long sv_v = (long)p.NDT * NE, sv_t = (long)p.nwg * p.nsave * sv_v;
+  const long wx_off = ((long)el.b * T) * GW * N * D + (long)tm.n * D + el.d;  // + t * GW*N*D + g * N*D
+  const long wx_t = (long)GW * N * D, wx_g = (long)N * D;
+  const bool has_ds = a.d_states != nullptr;
+  auto load_in = [&](int it, u32x4 (&dst)[NIN]) {
+    const long t = T - 1 - it;
 #pragma unroll
-  for (int q = 0; q < IOQ; ++q) {
-    e0[q] = io_elem(tm.lane, 4 * q);
-    el[q] = elem_of(p, tm, e0[q]);
-  }
-  auto load_in = [&](int it, u32x4 (&dst)[IOQ][NIN]) {
-    const int t = T - 1 - it;
+    for (int k = 0; k < S; ++k)
+      dst[k] = (el.real && has_ds && (k == 0 || !hidden_only)) ? ld4s<OS>(a.d_states, ds_off + k * ds_k + t * ds_t)
+                                                               : u32x4{0u, 0u, 0u, 0u};
 #pragma unroll
-    for (int q = 0; q < IOQ; ++q) {
-#pragma unroll
-      for (int k = 0; k < S; ++k)
-        dst[q][k] = (el[q].real && a.d_states && (k == 0 || !hidden_only))
-                        ? ld4_raw(a.d_states, ((((long)k * B + el[q].b) * T + t) * N + tm.n) * D + el[q].d, p.dt_out)
-                        : u32x4{0u, 0u, 0u, 0u};
-#pragma unroll
-      for (int v = 0; v < NSAVE; ++v)
-        dst[q][S + v] = el[q].real  // padding rows were not saved
-                            ? *reinterpret_cast<const u32x4*>(a.save + save_index(p, NE, t, tm.wgi, v, tm.team, e0[q]))
-                            : u32x4{0u, 0u, 0u, 0u};
-    }
+    for (int v = 0; v < NSAVE; ++v)
+      dst[S + v] = el.real  // padding rows were not saved
+                       ? ld4s<SS>(a.save, sv_off + v * sv_v + t * sv_t)
+                       : u32x4{0u, 0u, 0u, 0u};
   };
-  auto stage = [&](int slot, const u32x4 (&src)[IOQ][NIN]) {
+  auto stage = [&](int it, const u32x4 (&src)[NIN]) {
+    float* slot = iring + (long)(it % kBwdStage) * NIN * NE;
 #pragma unroll
-    for (int q = 0; q < IOQ; ++q) {
-      f32x4 v[NIN];
-#pragma unroll
-      for (int k = 0; k < S; ++k) v[k] = raw4_f32(src[q][k], p.dt_out);
-#pragma unroll
-      for (int k = S; k < NIN; ++k) v[k] = __builtin_bit_cast(f32x4, src[q][k]);
-      // transpose: element e0+m gets its NOP values contiguous
-#pragma unroll
-      for (int m = 0; m < 4; ++m)
-#pragma unroll
-        for (int c = 0; c < NOP / 4; ++c) {
-          f32x4 o;
-#pragma unroll
-          for (int r = 0; r < 4; ++r) o[r] = (4 * c + r < NIN) ? v[4 * c + r < NIN ? 4 * c + r : 0][m] : 0.f;
-          *reinterpret_cast<f32x4*>(iring + ((long)slot * NE + e0[q] + m) * NOP + 4 * c) = o;
-        }
-    }
+    for (int k = 0; k < NIN; ++k)
+      *reinterpret_cast<f32x4*>(slot + k * NE + e0) = k < S ? cvt4s<OS>(src[k], of16) : cvt4s<SS>(src[k], sf16);
   };
   auto store_out = [&](int it, const float* src) {
-    const int t = T - 1 - it;
+    const long t = T - 1 - it;
+    f32x4 o[NOB];
 #pragma unroll
-    for (int q = 0; q < IOQ; ++q) {
-      if (!el[q].real) continue;
-      f32x4 in[4];
+    for (int g = 0; g < NOB; ++g) o[g] = *reinterpret_cast<const f32x4*>(src + g * NE + e0);
+    if (!el.real) return;
 #pragma unroll
-      for (int m = 0; m < 4; ++m) in[m] = *reinterpret_cast<const f32x4*>(src + (e0[q] + m) * NOB);
-#pragma unroll
-      for (int g = 0; g < GW; ++g)
-        st4(a.dwx, ((long)el[q].b * T + t) * wx_t + ((long)g * N + tm.n) * D + el[q].d, p.dt_io,
-            f32x4{in[0][g], in[1][g], in[2][g], in[3][g]});
-      if constexpr (CELL == CELL_GRU)  // the R-only candidate gate's cotangent, for the dR GEMM
-        *reinterpret_cast<f32x4*>(a.dcand + (((long)el[q].b * T + t) * N + tm.n) * D + el[q].d) =
-            f32x4{in[0][3], in[1][3], in[2][3], in[3][3]};
-    }
+    for (int g = 0; g < GW; ++g) st4s<XS>(a.dwx, wx_off + t * wx_t + g * wx_g, o[g], xf16);
+    if constexpr (CELL == CELL_GRU)  // the R-only candidate gate's cotangent, for the dR GEMM
+      *reinterpret_cast<f32x4*>(a.dcand + ((long)el.b * T + t) * N * D + (long)tm.n * D + el.d) = o[3];
   };
 
   Prof prof;
   prof.init(a.prof != nullptr && blockIdx.x == 0, a.prof != nullptr);
-  u32x4 buf[P][IOQ][NIN];
+  u32x4 buf[PR][NIN];  // indexed with constants only (unrolled loops), so it stays in registers
 #pragma unroll
-  for (int j = 0; j < P; ++j)
+  for (int j = 0; j < PR; ++j)
     if (j < T) load_in(j, buf[j]);
-  stage(0, buf[0]);
-  if (P < T) load_in(P, buf[0]);
-  lds_barrier();  // iteration 0's inputs staged
-  for (int it0 = 0; it0 < T; it0 += P) {
 #pragma unroll
-    for (int j = 0; j < P; ++j) {
+  for (int j = 0; j < PR; ++j) {
+    if (j < T) stage(j, buf[j]);
+    if (j + PR < T) load_in(j + PR, buf[j]);
+  }
+  lds_barrier();  // inputs of iterations 0 and 1 staged
+  for (int it0 = 0; it0 < T; it0 += PR) {
+#pragma unroll
+    for (int j = 0; j < PR; ++j) {
       const int it = it0 + j;
       if (it < T) {
-        const int jn = (j + 1) % P;
-        if (it + 1 < T) {
-          stage(jn, buf[jn]);
+        if (it + PR < T) {
+          stage(it + PR, buf[j]);  // buf[j] holds iteration it + 2 (loaded two iterations ago)
           prof.mark(0);
           prof.stamp(it, 0);
-          if (it + 1 + P < T) load_in(it + 1 + P, buf[jn]);
+          if (it + 2 * PR < T) load_in(it + 2 * PR, buf[j]);
           prof.mark(1);
           prof.stamp(it, 1);
         }
-        lds_barrier();  // iteration it: outputs staged; inputs of it+1 staged
+        lds_barrier();  // iteration it: outputs staged; inputs of it+2 staged
         prof.mark(2);
         prof.stamp(it, 2);
         store_out(it, ost + (long)(it & 1) * NOB * NE);
@@ -1052,7 +1078,9 @@ __device__ void bwd_scout(const BwdArgs& a, const Team& tm, float* lds) {
   const int b0 = tm.slab * p.BS, nreal = min(p.BS, B - b0);
   const int row_bytes = D * esz, lpr = (row_bytes + 127) / 128 + 1;  // lines of one row (+1: unaligned rows)
   const int nd = nst * nreal * lpr;                                    // state-cotangent touches
-  const int ns = p.wpg * p.nsave * p.NDT * p.NB * 8;                   // save touches (8 lines per 16-row tile)
+  const int ssz = p.dt_save == DT_F32 ? 4 : 2;                         // bytes of a saved value
+  const int lpt = 2 * ssz;                                             // lines of a 16-row tile of one value
+  const int ns = p.wpg * p.nsave * p.NDT * p.NB * lpt;                 // save touches
   auto lptr = (__attribute__((address_space(3))) void*)(lds + (threadIdx.x >> 6) * 64);
   auto touch = [&](int it) {
     const int t = T - 1 - it;
@@ -1063,12 +1091,12 @@ __device__ void bwd_scout(const BwdArgs& a, const Team& tm, float* lds) {
         const long e0 = ((((long)k * B + b0 + r) * T + t) * N + tm.n) * D;
         src = static_cast<const char*>(a.d_states) + e0 * esz + min(128 * l, row_bytes - 4);
       } else {
-        const int j = i - nd, l = j & 7, bt = (j >> 3) % p.NB, rest = (j >> 3) / p.NB;
+        const int j = i - nd, l = j % lpt, bt = (j / lpt) % p.NB, rest = (j / lpt) / p.NB;
         const int team = rest % p.NDT, v = (rest / p.NDT) % p.nsave, m = rest / (p.NDT * p.nsave);
         const int rows = min(max(nreal - bt * 16, 0), 16);  // real rows of this 16-row tile
-        if (2 * l < rows)  // a 128-byte line holds two rows of 16 units
-          src = reinterpret_cast<const char*>(a.save + save_index(p, NE, t, tm.group * p.wpg + m, v, team, bt * 256) +
-                                              32 * l);
+        if (l * (8 / ssz) < rows)  // a 128-byte line holds 8 / ssz rows of 16 units
+          src = static_cast<const char*>(a.save) +
+                save_index(p, NE, t, tm.group * p.wpg + m, v, team, bt * 256) * ssz + 128 * l;
       }
       if (src) __builtin_amdgcn_global_load_lds(src, lptr, 4, 0, 0);
     }
@@ -1107,8 +1135,8 @@ __global__ void __launch_bounds__(64 * (KSC + 1) * NDT) bwd_kernel(BwdArgs a) {
   using CS = CellShape<CELL>;
   constexpr int GR = CS::GR, GW = CS::GW, GT = CS::GT, S = CS::S;
   constexpr int NE = NB * 256, EPLMAX = (4 * NB + KSC - 1) / KSC, KS = KSC;
-  constexpr int NSAVE = Cell<CELL>::NSAVE, P = BwdRing<CELL>::P;
-  constexpr int NOP = Lds<CELL, NB>::NOP, NOB = Lds<CELL, NB>::NOB;
+  constexpr int NSAVE = Cell<CELL>::NSAVE, NIN = S + NSAVE;
+  constexpr int NOB = Lds<CELL, NB>::NOB;
   constexpr int NF = GR * KTW;  // max fragments of R^T per wave
   const Plan& p = a.p;
   extern __shared__ float lds[];
@@ -1134,11 +1162,17 @@ __global__ void __launch_bounds__(64 * (KSC + 1) * NDT) bwd_kernel(BwdArgs a) {
 
   constexpr int RED_B = Lds<CELL, NB>::RED_B;
   float* red = lds + tm.team * Lds<CELL, NB>::bwd(KS);  // [2][NB][KS][304]
-  float* iring = red + 2L * NB * KS * RED_B;             // [P][NE][NOP]
-  float* ost = iring + (long)P * NE * NOP;               // [2][NE][NOB]
+  float* iring = red + 2L * NB * KS * RED_B;             // [3][NIN][NE]
+  float* ost = iring + (long)kBwdStage * NIN * NE;       // [2][NOB][NE]
 
   if (tm.kw == KS) {
-    bwd_io<CELL, MMA, NB>(a, tm, iring, ost);
+    // saved values: FP16 under the 16-bit policies (sLSTM: FP32), FP32 with FP32 operands
+    constexpr int SS = SaveSize<CELL, MMA>::value;
+    switch (io_sizes(p.dt_io, p.dt_out)) {
+      case 0: bwd_io<CELL, MMA, NB, 2, 2, SS>(a, tm, iring, ost); break;
+      case 1: bwd_io<CELL, MMA, NB, 2, 4, SS>(a, tm, iring, ost); break;
+      default: bwd_io<CELL, MMA, NB, 4, 4, SS>(a, tm, iring, ost); break;
+    }
     return;
   }
 
@@ -1216,25 +1250,35 @@ __global__ void __launch_bounds__(64 * (KSC + 1) * NDT) bwd_kernel(BwdArgs a) {
   Prof prof;
   prof.init(a.prof != nullptr && blockIdx.x == 0, a.prof != nullptr);
   __builtin_amdgcn_s_waitcnt(0);  // no set-up load pending at the loop head (see the forward kernel)
-  lds_barrier();  // iteration 0's inputs staged by the I/O wave
+  lds_barrier();  // inputs of iterations 0 and 1 staged by the I/O wave
+  // One-tile workgroups read the owners' inputs of the next iteration from LDS
+  // during this iteration's poll (the I/O wave staged them before the previous
+  // barrier), so no LDS read stands between the loop head and the pointwise
+  // backward. Two-tile workgroups (two elements per lane, 256 registers a wave)
+  // have no registers for a second set and read them at the loop head.
+  constexpr bool kPrefetch = NDT == 1;
+  float in_cur[EPLMAX][NIN], in_next[kPrefetch ? EPLMAX : 1][NIN];
+  auto read_in = [&](int it, auto& dst) {
+    const float* ir = iring + (long)(it % kBwdStage) * NIN * NE;
+#pragma unroll
+    for (int s = 0; s < EPLMAX; ++s)
+#pragma unroll
+      for (int k = 0; k < NIN; ++k) dst[s][k] = own[s] ? ir[k * NE + oe[s]] : 0.f;
+  };
+  read_in(0, in_cur);
   bool abort = false;
   for (int it = 0; it < T; ++it) {
     prof.stamp(it, 0);
     const int xoff = (it & 1) * xpar;
+    if constexpr (!kPrefetch)
+      if (it > 0) read_in(it, in_cur);
     // ---- 1. owners: pointwise backward of step t = T-1-it, publish dG_t
-    const float* ir = iring + (long)(it % P) * NE * NOP;
     float* os = ost + (long)(it & 1) * NE * NOB;
 #pragma unroll
     for (int s = 0; s < EPLMAX; ++s) {
       if (!own[s]) continue;
       const int e = oe[s];
-      float in[NOP];
-#pragma unroll
-      for (int c = 0; c < NOP / 4; ++c) {
-        const f32x4 v = *reinterpret_cast<const f32x4*>(ir + e * NOP + 4 * c);
-#pragma unroll
-        for (int r = 0; r < 4; ++r) in[4 * c + r] = v[r];
-      }
+      const float* in = in_cur[s];
       float ds[S];
 #pragma unroll
       for (int k = 0; k < S; ++k) ds[k] = carry[s][k] + in[k];
@@ -1265,12 +1309,7 @@ __global__ void __launch_bounds__(64 * (KSC + 1) * NDT) bwd_kernel(BwdArgs a) {
       }
 #pragma unroll
       for (int k = 0; k < S; ++k) carry[s][k] = cr[k];
-      f32x4 ov = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int g = 0; g < GW; ++g) ov[g] = dwx[g];
-      if constexpr (CELL == CELL_GRU) ov[3] = dry[0];
-      *reinterpret_cast<f32x4*>(os + e * NOB) = ov;
-      // the element's gate cotangents go out last (k = o * GR + g: one vector store when GR = 4)
+      // the element's gate cotangents go out first (k = o * GR + g: one vector store when GR = 4)
       if (el[s].real && !cut) {
         if constexpr (MMA != MMA_F32 && GR == 4) {  // k = 4d .. 4d+3: one aligned chunk
           xstore_vec<MMA, GR, kSplit>(xc, xoff + xgrp + xword_of<MMA>(p.BS, el[s].bl, el[s].d * GR), dry,
@@ -1282,6 +1321,10 @@ __global__ void __launch_bounds__(64 * (KSC + 1) * NDT) bwd_kernel(BwdArgs a) {
                                 step_tag(it));
         }
       }
+      // then the outputs the I/O wave drains after the barrier (value-major)
+#pragma unroll
+      for (int g = 0; g < GW; ++g) os[g * NE + e] = dwx[g];
+      if constexpr (CELL == CELL_GRU) os[3 * NE + e] = dry[0];
     }
     prof.mark(3);
     prof.stamp(it, 1);
@@ -1296,14 +1339,21 @@ __global__ void __launch_bounds__(64 * (KSC + 1) * NDT) bwd_kernel(BwdArgs a) {
     // accumulator for the lo products measured slower)
     auto prod = [&](int bt, int j, const Frag<MMA>& f, int) { acc[bt] = mma(A[j], f, acc[bt]); };
     uint32_t polls = 0;
-    if (cut)  // gradient_recurrent_cut: no R^T dG reaches h_{t-1}
+    // the next iteration's inputs, read while the first poll is in flight
+    auto between = [&]() {
+      if constexpr (kPrefetch)
+        if (it + 1 < T) read_in(it + 1, in_next);
+    };
+    if (cut) {  // gradient_recurrent_cut: no R^T dG reaches h_{t-1}
       zero();
-    else if (NB == 1 && pair)
-      polls = gather_pair_mma<MMA, NDT, NF, kSplit, kSpecB>(xc, xword_pair, bv_pair, xoff, cstride, nkt,
-                                                            ptag(p, it), a.status, a.spin_limit, abort, zero, prod);
-    else
+      between();
+    } else if (NB == 1 && pair) {
+      polls = gather_pair_mma<MMA, NDT, NF, kSplit, kSpecB>(xc, xword_pair, bv_pair, xoff, cstride, nkt, ptag(p, it),
+                                                            a.status, a.spin_limit, abort, zero, prod, between);
+    } else {
       polls = gather_mma<MMA, NDT, NB, NF, kSplit, kSpecB>(xc, xword, bval, xoff, cstride, nkt, ptag(p, it),
-                                                           a.status, a.spin_limit, abort, zero, prod);
+                                                           a.status, a.spin_limit, abort, zero, prod, between);
+    }
     // paired split-word products: columns 8-15 hold the lo products of rows 0-7
     if constexpr (kSplit && NB == 1)
       if (pair && !cut) acc[0] = fold_cols8(acc[0]);
@@ -1332,6 +1382,12 @@ __global__ void __launch_bounds__(64 * (KSC + 1) * NDT) bwd_kernel(BwdArgs a) {
       for (int w2 = 0; w2 < KS; ++w2) v += part[w2];
       // the BF16 policy rounds the cotangent of the rounded hidden operand
       dhrec[s] = el[s].real ? round_op<MMA>(v) : 0.f;
+    }
+    if constexpr (kPrefetch) {
+#pragma unroll
+      for (int s = 0; s < EPLMAX; ++s)
+#pragma unroll
+        for (int k = 0; k < NIN; ++k) in_cur[s][k] = in_next[s][k];
     }
     prof.mark(6);
     prof.stamp(it, 4);
