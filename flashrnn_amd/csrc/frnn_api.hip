@@ -597,6 +597,16 @@ int frnn_status(const void* ws, frnn_stream_t stream) {
   return v == 0 ? FRNN_OK : -(int)v;
 }
 
+// Test hook (declared in frnn_plan.h, not part of the public ABI): the launch
+// plan of a problem, for the host bounds check of the kernels' addressing.
+int frnn_test_plan(const frnn_desc* d, void* plan_out, size_t bytes) {
+  if (!plan_out || bytes != sizeof(Plan)) return FRNN_E_INVALID;
+  Plan p;
+  const int rc = make_plan(d, &p);
+  if (rc == FRNN_OK) std::memcpy(plan_out, &p, sizeof(Plan));
+  return rc;
+}
+
 const char* frnn_strerror(int code) {
   switch (code) {
     case FRNN_OK: return "ok";

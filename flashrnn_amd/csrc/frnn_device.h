@@ -16,6 +16,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "frnn_plan.h"
+
 namespace frnn {
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
@@ -354,9 +356,7 @@ template <int MMA> struct XLayout {
 };
 template <int MMA>
 __device__ __forceinline__ int xword_of(int BS, int r, int k) {
-  constexpr int WP = XLayout<MMA>::WP, NC = XLayout<MMA>::NC;
-  const int kt = k >> 5, kq = (k >> 3) & 3, c = (k & 7) / WP, e = k % WP;
-  return (((kt * 4 + kq) * NC + c) * BS + r) * WP + e;
+  return xword_rt(XLayout<MMA>::WP, BS, r, k);
 }
 
 // Issue the loads of one 8-word run (8 consecutive k) whose first chunk is at

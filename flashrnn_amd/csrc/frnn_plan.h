@@ -9,7 +9,10 @@
 // saved-for-backward area can be laid out exactly as the lanes own it.
 #pragma once
 
+#include <stddef.h>
 #include <stdint.h>
+
+struct frnn_desc;
 
 namespace frnn {
 
@@ -94,4 +97,83 @@ inline int scout_blocks(const Plan& p) {
   return (p.flags & kFlagScout) ? kXcds * ((p.gcount + kXcds - 1) / kXcds) : 0;
 }
 
+// ---------------------------------------------------------------- addressing
+// Index arithmetic of the kernels' global and exchange accesses, shared with
+// the host bounds check (tests/bounds): every element or word a kernel touches
+// is computed by one of these functions.
+#if defined(__HIPCC__)
+#define FRNN_HD __host__ __device__
+#else
+#define FRNN_HD
+#endif
+
+// I/O lane `lane`, its i-th element: e = 256*(i/4) + 4*lane + i%4 (four
+// consecutive hidden units of one batch row per lane and batch tile).
+FRNN_HD inline int io_elem(int lane, int i) { return 256 * (i >> 2) + 4 * lane + (i & 3); }
+
+// Element e of hidden tile dt of slab `slab` -> hidden unit d, slab row bl, batch row b.
+struct ElemPos {
+  int d, bl, b;
+  bool real;
+};
+FRNN_HD inline ElemPos elem_pos(const Plan& p, int slab, int dt, int e) {
+  ElemPos x;
+  const int bt = e >> 8, r = e & 255;
+  x.d = dt * 16 + (r & 15);
+  x.bl = bt * 16 + (r >> 4);
+  x.b = slab * p.BS + x.bl;
+  x.real = x.b < p.B;
+  return x;
+}
+
+// Forward I/O lane's Wx DMA of window step u, gate g: element index of the
+// first of the 16 bytes it reads (4 FP32 or 8 16-bit units of one row), and
+// whether the lane reads at all (real row; 16-bit rows use the even quads).
+FRNN_HD inline long wx_dma_index(const Plan& p, int slab, int n, int dt, int lane, int u, int g, int esz, bool* valid) {
+  const int lrow = lane >> 2, lquad = lane & 3;
+  const int lb = slab * p.BS + lrow;
+  *valid = lb < p.B && (esz == 4 || (lquad & 1) == 0);
+  const long wx_t = (long)p.GW * p.N * p.D;
+  return ((long)lb * p.Ttot + p.t0 + u) * wx_t + ((long)g * p.N + n) * p.D + dt * 16 + 4 * lquad;
+}
+
+// State k of batch row b at window step t, head n, unit d: index into the
+// state output [nst][B][Ttot][N][D].
+FRNN_HD inline long state_index(const Plan& p, int k, int b, int t, int n, int d) {
+  return ((((long)k * p.B + b) * p.Ttot + p.t0 + t) * p.N + n) * p.D + d;
+}
+// The FRNN_OUT_LAST output [B][1][N][D].
+FRNN_HD inline long last_index(const Plan& p, int b, int n, int d) { return ((long)b * p.N + n) * p.D + d; }
+// Initial state / carry / their cotangents [S][B][N][D].
+FRNN_HD inline long carry_index(const Plan& p, int k, int b, int n, int d) {
+  return (((long)k * p.B + b) * p.N + n) * p.D + d;
+}
+
+// Lane-native saved values: [t][workgroup][value][team*NE + e].
+FRNN_HD inline long save_index(const Plan& p, int ne, int t, int wgi, int v, int team, int e) {
+  const long per = (long)p.NDT * ne;
+  return (((long)t * p.nwg + wgi) * p.nsave + v) * per + (long)team * ne + e;
+}
+
+// Exchange word of (row r, contraction index k) in one group's table, chunk-major
+// with wp words per 16-byte chunk (see XLayout in frnn_device.h).
+FRNN_HD inline int xword_rt(int wp, int BS, int r, int k) {
+  const int nc = 8 / wp;
+  const int kt = k >> 5, kq = (k >> 3) & 3, c = (k & 7) / wp, e = k % wp;
+  return (((kt * 4 + kq) * nc + c) * BS + r) * wp + e;
+}
+
+// Forward scout touch: byte offset into Wx of line l of (slab row r, window
+// step u, gate g); a row's lines are clamped to its last 4 bytes.
+FRNN_HD inline long scout_wx_byte(const Plan& p, int slab, int n, int r, int u, int g, int l, int esz) {
+  const long e0 = ((((long)(slab * p.BS + r) * p.Ttot + p.t0 + u) * p.GW + g) * p.N + n) * p.D;
+  const int row_bytes = p.D * esz;
+  return e0 * esz + (128 * l < row_bytes - 4 ? 128 * l : row_bytes - 4);
+}
+
 }  // namespace frnn
+
+// Test hook of libfrnn.so (not part of the public ABI in include/frnn.h): copies
+// the launch plan of *d (a frnn_desc) into plan_out (bytes == sizeof(frnn::Plan)),
+// for the host bounds check; returns make_plan's code.
+extern "C" int frnn_test_plan(const struct frnn_desc* d, void* plan_out, size_t bytes);

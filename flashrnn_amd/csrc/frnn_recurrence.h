@@ -20,7 +20,8 @@
 //
 // Element e of a team (0 <= e < 256*NB) is (batch tile e>>8, hidden unit
 // e&15 of the tile, batch row (e>>4)&15). Compute lane (kw, lane) owns the
-// elements e = s*KS*64 + kw*64 + lane; I/O lane l serves e = l + 64*i.
+// elements e = s*KS*64 + kw*64 + lane; I/O lane l serves e = io_elem(l, i)
+// (frnn_plan.h).
 #pragma once
 
 #include "frnn_cells.h"
@@ -159,19 +160,8 @@ __device__ __forceinline__ bool scout_setup(const Plan& p, Team& tm, uint32_t* c
 }
 
 // Element e of the team -> hidden unit d, slab row bl, batch row b.
-struct Elem {
-  int d, bl, b;
-  bool real;
-};
-__device__ __forceinline__ Elem elem_of(const Plan& p, const Team& tm, int e) {
-  Elem x;
-  const int bt = e >> 8, r = e & 255;
-  x.d = tm.dt * 16 + (r & 15);
-  x.bl = bt * 16 + (r >> 4);
-  x.b = tm.slab * p.BS + x.bl;
-  x.real = x.b < p.B;
-  return x;
-}
+typedef ElemPos Elem;
+__device__ __forceinline__ Elem elem_of(const Plan& p, const Team& tm, int e) { return elem_pos(p, tm.slab, tm.dt, e); }
 // Position of element e in the MFMA output layout of its batch tile: lane
 // (dd/4)*16 + row, register dd%4 (dd = hidden unit in the tile), as lane*4 + reg.
 __device__ __forceinline__ int mfma_pos(int e) {
@@ -179,11 +169,6 @@ __device__ __forceinline__ int mfma_pos(int e) {
   return ((dd >> 2) * 16 + bb) * 4 + (dd & 3);
 }
 
-// Lane-native saved values: [t][workgroup][value][team*NE + e].
-__device__ __forceinline__ long save_index(const Plan& p, int ne, int t, int wgi, int v, int team, int e) {
-  const long per = (long)p.NDT * ne;
-  return (((long)t * p.nwg + wgi) * p.nsave + v) * per + (long)team * ne + e;
-}
 
 // Phase profile of every wave of workgroup 0 (8 words per wave). Compute
 // waves: cycles in [0] exchange wait, [1] MFMA + LDS partials, [2] barrier,
@@ -508,11 +493,9 @@ template <int CELL, int MMA> struct SaveSize {
 };
 
 // ====================================================================== forward
-// I/O lane l serves the elements e = 256*(i/4) + 4*l + i%4: four consecutive
-// hidden units of one batch row, so every global access is one 8/16-byte
-// vector access and every LDS access one 16-byte access.
-__device__ __forceinline__ int io_elem(int lane, int i) { return 256 * (i >> 2) + 4 * lane + (i & 3); }
-
+// I/O lane l serves the elements io_elem(l, i) = 256*(i/4) + 4*l + i%4: four
+// consecutive hidden units of one batch row, so every global access is one
+// 8/16-byte vector access and every LDS access one 16-byte access.
 
 // I/O wave of a team. Wx of step u is loaded straight into raw slot u % 2 by
 // LDS-DMA (global_load_lds: no registers in flight), three steps ahead; two
@@ -545,9 +528,8 @@ __device__ void fwd_io(const FwdArgs& a, const Team& tm, float* xring, float* os
   const long wx_t = (long)GW * N * D;
   // loads: lane -> (row, quad); 16-bit chunks hold 8 units, so odd quads idle
   const int lrow = tm.lane >> 2, lquad = tm.lane & 3;
-  const int lb = tm.slab * p.BS + lrow;
-  const bool lval = lb < B && (XS == 4 || (lquad & 1) == 0);
-  const long lbase = ((long)lb * TT + t0) * wx_t + (long)tm.n * D + tm.dt * 16 + 4 * lquad;
+  bool lval;
+  const long lbase = wx_dma_index(p, tm.slab, tm.n, tm.dt, tm.lane, 0, 0, XS, &lval);  // + u * wx_t + g * N * D
   auto load_wx = [&](int u) {
     float* slot = xring + (long)(u % kFwdRing) * RING;
 #pragma unroll
@@ -563,14 +545,14 @@ __device__ void fwd_io(const FwdArgs& a, const Team& tm, float* xring, float* os
   const Elem el = elem_of(p, tm, e0);
   long st_off[S];
 #pragma unroll
-  for (int k = 0; k < S; ++k) st_off[k] = ((((long)k * B + el.b) * TT + t0) * N + tm.n) * D + el.d;
-  const long st_step = (long)N * D;
+  for (int k = 0; k < S; ++k) st_off[k] = state_index(p, k, el.b, 0, tm.n, el.d);
+  const long st_step = (long)N * D;  // state_index per window step
   const long sv_off = save_index(p, NE, 0, tm.wgi, 0, tm.team, e0);
-  const long sv_per = (long)p.NDT * NE, sv_step = (long)p.nwg * p.nsave * sv_per;
+  const long sv_per = (long)p.NDT * NE, sv_step = (long)p.nwg * p.nsave * sv_per;  // save_index per value, step
   auto store_out = [&](int t, const float* src) {
     if (mode == 2) {  // [B,1,N,D]: the last step of the sequence only
       if (t0 + t == TT - 1 && el.real)
-        st4s<OS>(a.states, ((long)el.b * N + tm.n) * D + el.d, *reinterpret_cast<const f32x4*>(src + e0), of16);
+        st4s<OS>(a.states, last_index(p, el.b, tm.n, el.d), *reinterpret_cast<const f32x4*>(src + e0), of16);
       return;
     }
     // every staged value is read (unused ones too), so the reads form one burst
@@ -676,9 +658,8 @@ __device__ void fwd_scout(const FwdArgs& a, const Team& tm, float* lds) {
   auto touch = [&](int u) {
     for (int i = threadIdx.x; i < nt; i += blockDim.x) {
       const int r = i / (GW * lpr), g = (i / lpr) % GW, l = i % lpr;
-      const long e0 = ((((long)(b0 + r) * p.Ttot + p.t0 + u) * GW + g) * N + tm.n) * D;
-      __builtin_amdgcn_global_load_lds(static_cast<const char*>(a.wx) + e0 * esz + min(128 * l, row_bytes - 4), lptr,
-                                       4, 0, 0);
+      __builtin_amdgcn_global_load_lds(static_cast<const char*>(a.wx) + scout_wx_byte(p, tm.slab, tm.n, r, u, g, l, esz),
+                                       lptr, 4, 0, 0);
     }
   };
   const char* xw = a.xbuf + (long)tm.group * p.BS * D * (MMA == MMA_F32 ? 8 : 4);
@@ -807,7 +788,7 @@ __global__ void __launch_bounds__(64 * (KSC + 1) * NDT) fwd_kernel(FwdArgs a) {
     el[s].real = el[s].real && own[s];
 #pragma unroll
     for (int k = 0; k < S; ++k)
-      st[s][k] = el[s].real ? ld_val(a.s0, (((long)k * B + el[s].b) * N + tm.n) * D + el[s].d, p.dt_state) : 0.f;
+      st[s][k] = el[s].real ? ld_val(a.s0, carry_index(p, k, el[s].b, tm.n, el[s].d), p.dt_state) : 0.f;
 #pragma unroll
     for (int g = 0; g < GT; ++g) bias[s][g] = own[s] ? ld_val(a.bias, ((long)g * N + tm.n) * D + el[s].d, p.dt_io) : 0.f;
   }
@@ -952,7 +933,7 @@ __global__ void __launch_bounds__(64 * (KSC + 1) * NDT) fwd_kernel(FwdArgs a) {
       if (el[s].real)
 #pragma unroll
         for (int k = 0; k < S; ++k)
-          st_val(a.carry, (((long)k * B + el[s].b) * N + tm.n) * D + el[s].d, p.dt_state, st[s][k]);
+          st_val(a.carry, carry_index(p, k, el[s].b, tm.n, el[s].d), p.dt_state, st[s][k]);
   }
   prof.acc[5] = T;
   prof.flush(a.prof);
@@ -1240,7 +1221,7 @@ __global__ void __launch_bounds__(64 * (KSC + 1) * NDT) bwd_kernel(BwdArgs a) {
 #pragma unroll
     for (int k = 0; k < S; ++k)
       carry[s][k] = (el[s].real && a.d_carry)
-                        ? ld_val(a.d_carry, (((long)k * B + el[s].b) * N + tm.n) * D + el[s].d, p.dt_state)
+                        ? ld_val(a.d_carry, carry_index(p, k, el[s].b, tm.n, el[s].d), p.dt_state)
                         : 0.f;
     dhrec[s] = 0.f;
 #pragma unroll
@@ -1400,7 +1381,7 @@ __global__ void __launch_bounds__(64 * (KSC + 1) * NDT) bwd_kernel(BwdArgs a) {
     if (el[s].real) {
 #pragma unroll
       for (int k = 0; k < S; ++k)
-        st_val(a.ds0, (((long)k * B + el[s].b) * N + tm.n) * D + el[s].d, p.dt_state,
+        st_val(a.ds0, carry_index(p, k, el[s].b, tm.n, el[s].d), p.dt_state,
                carry[s][k] + (k == 0 ? dhrec[s] : 0.f));
     }
 #pragma unroll
