@@ -235,6 +235,22 @@ int make_plan(const frnn_desc* d, Plan* p) {
   const long long wsz = p->mma == FRNN_MMA_F32 ? 8 : 4;
   p->xwords_fwd = (long long)p->ngroups * p->BS * p->D;
   p->xwords_bwd = (long long)p->ngroups * p->BS * p->GR * p->D;
+  // Reduce-scatter backward (frnn_bwd_rs.h) for two-tile workgroups, where it is
+  // built: measured at B16 T1024 D768 it takes the LSTM backward from 16.2 to
+  // 8.6 ms and the GRU's (T512) from 5.0 to 4.4 ms, while at one-tile widths it
+  // is 2-3x slower than the all-gather (B8 T1024 N3 D256: 4.1 against 1.6 ms).
+  // FRNN_BWD_RS=0 (environment, read per plan) keeps the all-gather. Its table
+  // holds D * 16 * wpg 32-bit words per group and parity.
+  {
+    const int ntile = p->D / 16, ncw = p->NDT * p->KSB;
+    const int need = (ntile + ncw - 1) / ncw;
+    p->ptm = need <= 2 ? 2 : (need <= 4 ? 4 : (need <= 8 ? 8 : (need <= 16 ? 16 : 0)));
+    const char* e = std::getenv("FRNN_BWD_RS");
+    const bool off = e && *e == '0';
+    p->rs = (!off && p->NDT == 2 && p->ptm && p->wpg <= 32 &&
+             frnn::rs_kernel(p->cell, p->mma, p->NDT, p->KSB, p->ptm) != nullptr) ? 1 : 0;
+    if (p->rs) p->xwords_bwd = (long long)p->ngroups * p->D * 16 * p->wpg;
+  }
   p->save_floats = (long long)p->T * p->nwg * p->nsave * p->NDT * 256 * p->NB;
   // dR GEMM: 64x64 workgroup tiles where D % 64 == 0 (else 32x32), split over
   // K = B*T to fill the GPU (~2048 workgroups, >= 8 k-steps of 32 each): the
@@ -255,7 +271,7 @@ int make_plan(const frnn_desc* d, Plan* p) {
   const long long nclaim = 2LL * p->ngroups * frnn::kXcds * 4;
   p->off_claim_f = align_up(p->off_x + 2 * p->xwords_fwd * wsz);
   p->ws_fwd = align_up(p->off_claim_f + nclaim);
-  p->off_claim_b = align_up(p->off_x + 2 * p->xwords_bwd * wsz);
+  p->off_claim_b = align_up(p->off_x + 2 * p->xwords_bwd * (p->rs ? 4 : wsz));
   p->off_dcand = align_up(p->off_claim_b + nclaim + 256);  // + 256 zero bytes (dR GEMM's DMA tail source)
   const long long ndcand = p->cell == FRNN_GRU ? (long long)p->B * p->T * p->N * p->D : 0;
   p->off_part = align_up(p->off_dcand + ndcand * 4);
@@ -265,7 +281,7 @@ int make_plan(const frnn_desc* d, Plan* p) {
   // state and of the GRU's FP32 candidate-gate cotangents
   p->dma_gemm = gemm_uses_dma(*p) ? 1 : 0;
   p->ws_bwd += s0_copy_bytes(*p) + cand_copy_bytes(*p);
-  if (2 * p->xwords_bwd * wsz > 0x7fffffffLL) return FRNN_E_UNSUPPORTED;  // buffer-descriptor range
+  if (2 * p->xwords_bwd * (p->rs ? 4 : wsz) > 0x7fffffffLL) return FRNN_E_UNSUPPORTED;  // buffer-descriptor range
   return FRNN_OK;
 }
 
@@ -506,12 +522,13 @@ int frnn_bwd(const frnn_desc* d, const void* R, const void* s0, const void* stat
   if (!R || !s0 || !states || !save || !dwx || !dR || !db || !ds0 || !ws) return FRNN_E_INVALID;
   if ((p.flags & FRNN_OUT_LAST) || p.Ttot != p.T || p.t0 != 0) return FRNN_E_INVALID;  // forward-only options
   if ((long long)ws_bytes < p.ws_bwd) return FRNN_E_WORKSPACE;
-  const void* fn =
-      frnn::recurrence_kernel(p.cell, p.mma, p.KSB, ktw_class((p.kt_fwd + p.KSB - 1) / p.KSB, p.NDT), p.NDT, false);
+  const void* fn = p.rs ? frnn::rs_kernel(p.cell, p.mma, p.NDT, p.KSB, p.ptm)
+                        : frnn::recurrence_kernel(p.cell, p.mma, p.KSB,
+                                                  ktw_class((p.kt_fwd + p.KSB - 1) / p.KSB, p.NDT), p.NDT, false);
   if (!fn) return FRNN_E_UNSUPPORTED;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   char* w = static_cast<char*>(ws);
-  const long long xbytes = 2 * p.xwords_bwd * (p.mma == FRNN_MMA_F32 ? 8 : 4);
+  const long long xbytes = 2 * p.xwords_bwd * (p.rs ? 4 : (p.mma == FRNN_MMA_F32 ? 8 : 4));
   if ((rc = clear(w + p.off_x, p.off_dcand - p.off_x, st)) != FRNN_OK) return rc;  // exchange and claims
   frnn::BwdArgs a;
   a.p = p;
@@ -529,7 +546,8 @@ int frnn_bwd(const frnn_desc* d, const void* R, const void* s0, const void* stat
   a.status = reinterpret_cast<uint32_t*>(w);
   a.spin_limit = g_spin_limit.load();
   a.prof = g_phase_prof.load();
-  size_t lds = (size_t)p.NDT * frnn::recurrence_lds_floats(p.cell, false, p.KSB) * sizeof(float);
+  size_t lds = (p.rs ? (size_t)frnn::rs_lds_floats(p.cell, p.NDT)
+                     : (size_t)p.NDT * frnn::recurrence_lds_floats(p.cell, false, p.KSB)) * sizeof(float);
   const int block = 64 * p.NDT * (p.KSB + 1);
   int per_launch = 0;
   if ((rc = set_lds_limit(fn, lds)) != FRNN_OK) return rc;

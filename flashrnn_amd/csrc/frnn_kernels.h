@@ -95,6 +95,35 @@ inline const void* recurrence_kernel(int cell, int mma, int ks, int ktw, int ndt
   }
   return nullptr;
 }
+// Reduce-scatter backward kernels (frnn_bwd_rs.h) for (mma, hidden tiles per
+// workgroup, compute waves per tile, output-tile class); null if not built.
+const void* lstm_rs_kernel(int mma, int ndt, int ks, int ptm);
+const void* gru_rs_kernel(int mma, int ndt, int ks, int ptm);
+const void* elman_rs_kernel(int mma, int ndt, int ks, int ptm);
+const void* slstm_rs_kernel(int mma, int ndt, int ks, int ptm);
+long lstm_rs_lds_floats(int ndt);
+long gru_rs_lds_floats(int ndt);
+long elman_rs_lds_floats(int ndt);
+long slstm_rs_lds_floats(int ndt);
+inline const void* rs_kernel(int cell, int mma, int ndt, int ks, int ptm) {
+  switch (cell) {
+    case 0: return lstm_rs_kernel(mma, ndt, ks, ptm);
+    case 1: return gru_rs_kernel(mma, ndt, ks, ptm);
+    case 2: return elman_rs_kernel(mma, ndt, ks, ptm);
+    case 3: return slstm_rs_kernel(mma, ndt, ks, ptm);
+  }
+  return nullptr;
+}
+inline long rs_lds_floats(int cell, int ndt) {
+  switch (cell) {
+    case 0: return lstm_rs_lds_floats(ndt);
+    case 1: return gru_rs_lds_floats(ndt);
+    case 2: return elman_rs_lds_floats(ndt);
+    case 3: return slstm_rs_lds_floats(ndt);
+  }
+  return 0;
+}
+
 // dR GEMM: wide = 64x64 workgroup tiles (4 waves, D % 64 == 0), else 32x32 (1 wave).
 const void* gemm_kernel(int mma, bool wide);
 const void* reduce_kernel();

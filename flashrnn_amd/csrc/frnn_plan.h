@@ -63,6 +63,8 @@ struct Plan {
   long long off_claim_f, off_claim_b; // workgroup slot counters: 8 per launch (one per XCD), by first group
   long long off_part, off_dbpart;     // backward: dR split-K partials, db partials
   int dma_gemm;                       // backward: the dR GEMM runs on the LDS-DMA kernel
+  int rs;                             // backward: reduce-scatter exchange (bwd_rs_kernel)
+  int ptm;                            // reduce-scatter: output tiles per compute wave (class)
 };
 
 // Group / tile of a workgroup; returns false for an idle workgroup.

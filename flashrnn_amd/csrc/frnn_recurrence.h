@@ -1048,7 +1048,9 @@ __device__ void bwd_io(const BwdArgs& a, const Team& tm, float* iring, float* os
 // never read). The scout paces itself by the exchange word that member 0
 // publishes each iteration; nothing waits for it, and every wait of its own is
 // bounded (spin limit, sticky status), so it always finishes.
-template <int CELL, int MMA>
+// RS: the reduce-scatter backward (frnn_bwd_rs.h), whose exchange table holds
+// 32-bit split words of partial sums, [v][p][b][w] per group.
+template <int CELL, int MMA, bool RS = false>
 __device__ void bwd_scout(const BwdArgs& a, const Team& tm, float* lds) {
   using CS = CellShape<CELL>;
   constexpr int S = CS::S, GR = CS::GR;
@@ -1082,13 +1084,14 @@ __device__ void bwd_scout(const BwdArgs& a, const Team& tm, float* lds) {
       if (src) __builtin_amdgcn_global_load_lds(src, lptr, 4, 0, 0);
     }
   };
-  // the word of (row 0, k 0) of the group's table, parity by parity
-  const char* xw = a.xbuf + (long)tm.group * p.BS * GR * D * (MMA == MMA_F32 ? 8 : 4);
-  const long xpar_b = (long)p.ngroups * p.BS * GR * D * (MMA == MMA_F32 ? 8 : 4);
+  // the word of (row 0, k 0) of the group's table (RS: of p 0, row 0, producer 0), parity by parity
+  const long tbl = RS ? (long)D * 16 * p.wpg * 4 : (long)p.BS * GR * D * (MMA == MMA_F32 ? 8 : 4);
+  const char* xw = a.xbuf + (long)tm.group * tbl;
+  const long xpar_b = (long)p.ngroups * tbl;
   auto published = [&](int it) {
     const char* w = xw + (it & 1) * xpar_b;
     uint32_t tag;
-    if constexpr (MMA == MMA_F32) tag = __hip_atomic_load(reinterpret_cast<const uint32_t*>(w) + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if constexpr (MMA == MMA_F32 && !RS) tag = __hip_atomic_load(reinterpret_cast<const uint32_t*>(w) + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     else tag = __hip_atomic_load(reinterpret_cast<const uint32_t*>(w), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) & 3u;
     return tag == step_tag(it);
   };

@@ -4,6 +4,7 @@
 // D/32 >= 8; one-tile workgroups (widths up to 512) use k-tile classes 1, 2, 4;
 // two-tile workgroups (widths 544-768) use classes 6 and 8 with KS = 3, BF16 only.
 #include "frnn_kernels.h"
+#include "frnn_bwd_rs.h"
 #include "frnn_recurrence.h"
 
 namespace frnn {
@@ -42,6 +43,31 @@ const void* slstm_kernel(int mma, int ks, int ktw, int ndt, bool forward) {
 
 long slstm_lds_floats(bool forward, int ks) {
   return forward ? Lds<CELL_SLSTM, 1>::fwd(ks) : Lds<CELL_SLSTM, 1>::bwd(ks);
+}
+
+template <int MMA, int NDT, int KS, int PTM>
+static const void* pick_rs() {
+  return reinterpret_cast<const void*>(&bwd_rs_kernel<CELL_SLSTM, MMA, NDT, KS, PTM>);
+}
+
+// Reduce-scatter backward: two-tile workgroups (widths 544-1024), where it
+// replaces the all-gather backward (see frnn_bwd_rs.h).
+template <int MMA>
+static const void* rs_by_shape(int ndt, int ks, int ptm) {
+  if (ndt == 2 && ks == 3 && ptm == 8) return pick_rs<MMA, 2, 3, 8>();
+  return nullptr;
+}
+
+const void* slstm_rs_kernel(int mma, int ndt, int ks, int ptm) {
+  switch (mma) {
+    case MMA_BF16: return rs_by_shape<MMA_BF16>(ndt, ks, ptm);
+    case MMA_F16: return rs_by_shape<MMA_F16>(ndt, ks, ptm);
+  }
+  return nullptr;
+}
+
+long slstm_rs_lds_floats(int ndt) {
+  return ndt == 1 ? RsShape<CELL_SLSTM, 1>::floats() : RsShape<CELL_SLSTM, 2>::floats();
 }
 
 }  // namespace frnn
