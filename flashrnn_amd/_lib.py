@@ -19,6 +19,7 @@ FRNN_MMA_BF16, FRNN_MMA_F32, FRNN_MMA_F16 = 0, 1, 2
 FRNN_TRAINING, FRNN_XCD_SHARED, FRNN_GRAD_CUT, FRNN_GRAD_CLIP, FRNN_TEST_UNREADY = 1, 2, 4, 8, 16
 FRNN_OUT_HIDDEN, FRNN_OUT_LAST, FRNN_SNAPSHOT_F32, FRNN_SLSTM_V1GRAD = 32, 64, 128, 256
 FRNN_OK = 0
+FRNN_E_INVALID, FRNN_E_UNSUPPORTED, FRNN_E_WORKSPACE, FRNN_E_LAUNCH = -1, -2, -3, -4
 FRNN_E_TIMEOUT = -5
 FRNN_E_PLACEMENT = -6
 FRNN_E_SCRATCH = -7
@@ -47,6 +48,7 @@ EXPORTS = (
     "frnn_cell_sizes",
     "frnn_workspace_bytes",
     "frnn_fwd",
+    "frnn_fwd_projected",
     "frnn_fwd_noalloc",
     "frnn_bwd",
     "frnn_status",
@@ -82,6 +84,8 @@ def load(path: str | os.PathLike | None = None) -> ctypes.CDLL:
     lib.frnn_workspace_bytes.restype = sz
     lib.frnn_fwd.argtypes = [dp, vp, vp, vp, vp, vp, vp, vp, vp, sz, vp]
     lib.frnn_fwd.restype = i32
+    lib.frnn_fwd_projected.argtypes = [dp, ctypes.c_int32, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, sz, vp]
+    lib.frnn_fwd_projected.restype = i32
     lib.frnn_fwd_noalloc.argtypes = [dp, vp, vp, vp, vp, vp, vp, vp, vp, vp]
     lib.frnn_fwd_noalloc.restype = i32
     lib.frnn_bwd.argtypes = [dp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, sz, vp]

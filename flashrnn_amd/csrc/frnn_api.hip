@@ -391,8 +391,57 @@ int clear(void* base, long long bytes, hipStream_t stream) {
 // counters at their offsets from `w`; the status word is `status`, which the
 // workspace's first word is for frnn_fwd). Clears the exchange and the counters,
 // then launches the persistent kernel(s). Allocates nothing.
+// ---- input projection (frnn_fwd_projected): its counters follow the forward
+// workspace -- ready[nrt] (column tiles done per row tile), then the tile counter
+long long proj_row_tiles(const Plan& p) { return ((long long)p.B * p.T + frnn::kProjRows - 1) / frnn::kProjRows; }
+long long proj_ws_bytes(const Plan& p) { return p.ws_fwd + align_up(4 * (proj_row_tiles(p) + 1)); }
+
+// FRNN_PROJ_OVERLAP=0 (environment, read per call): run the projection workers
+// in a launch of their own before the forward instead of beside it.
+bool proj_overlap_allowed() {
+  const char* e = std::getenv("FRNN_PROJ_OVERLAP");
+  return !(e && *e == '0');
+}
+
+// XCDs whose projection workers leave at once: with the XCD-local exchange,
+// group slot s of XCD x holds group s * 8 + x, so the first min(groups, 8) XCDs
+// host groups. Where every XCD does (or placement is free), none is skipped.
+uint32_t proj_skip_xcds(const Plan& p) {
+  if ((p.flags & FRNN_XCD_SHARED) || p.ngroups >= frnn::kXcds) return 0u;
+  return (1u << p.ngroups) - 1u;
+}
+
+// Projection workgroups that can run beside the recurrence in one launch of
+// the gated kernel `fg`: one workgroup per CU (more dynamic LDS than half a CU
+// holds, so a worker never shares a CU with a member and the recurrence keeps
+// its CUs to itself), every group in the one launch, and the CUs the
+// recurrence leaves free. Returns 0 where that does not hold; sets *lds.
+int proj_workers(const Plan& p, const void* fg, int block, long long tiles, size_t* lds) {
+  constexpr size_t kHalfCu = 80 * 1024;
+  const size_t l = *lds > kHalfCu ? *lds : kHalfCu + 1024;
+  if (set_lds_limit(fg, l) != FRNN_OK || blocks_per_cu(fg, block, l) != 1) return 0;
+  int per_launch = 0;
+  if (groups_per_launch(p, fg, block, l, &per_launch) != FRNN_OK || per_launch < p.ngroups) return 0;
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) {
+    (void)hipGetLastError();
+    return 0;
+  }
+  const int free_cus = cus - p.grid;
+  if (free_cus < frnn::kXcds) return 0;
+  *lds = l;
+  // With XCDs free of groups (proj_skip_xcds), one worker per CU of the whole
+  // GPU: the workers dispatched to an XCD with groups leave at once, and those
+  // of a free XCD fill its CUs once the recurrence's unused slots there have
+  // left. Otherwise the CUs the recurrence leaves, at most one worker wave per tile.
+  if (proj_skip_xcds(p)) return cus / frnn::kXcds * frnn::kXcds;
+  const long long useful = (tiles + block / 64 - 1) / (block / 64);
+  return (int)std::min<long long>(free_cus, useful);
+}
+
 int fwd_launch(const Plan& p, const void* wx, const void* R, const void* b, const void* s0, void* states_out,
-               void* carry_out, void* save, char* w, uint32_t* status, bool allow_timing, hipStream_t st) {
+               void* carry_out, void* save, char* w, uint32_t* status, bool allow_timing, hipStream_t st,
+               const frnn::ProjArgs* proj = nullptr) {
   if (!wx || !R || !b || !s0 || !states_out) return FRNN_E_INVALID;
   const bool training = (p.flags & FRNN_TRAINING) != 0;
   if (training && !save) return FRNN_E_INVALID;
@@ -401,8 +450,9 @@ int fwd_launch(const Plan& p, const void* wx, const void* R, const void* b, cons
   if (!fn) return FRNN_E_UNSUPPORTED;
   int rc;
   const long long xbytes = 2 * p.xwords_fwd * (p.mma == FRNN_MMA_F32 ? 8 : 4);
-  if ((rc = clear(w + p.off_x, p.ws_fwd - p.off_x, st)) != FRNN_OK) return rc;  // exchange and claims
-  frnn::FwdArgs a;
+  // exchange and claims (and the projection's counters)
+  if ((rc = clear(w + p.off_x, (proj ? proj_ws_bytes(p) : p.ws_fwd) - p.off_x, st)) != FRNN_OK) return rc;
+  frnn::FwdArgs a{};
   a.p = p;
   a.wx = wx;
   a.R = R;
@@ -422,6 +472,38 @@ int fwd_launch(const Plan& p, const void* wx, const void* R, const void* b, cons
   int per_launch = 0;
   if ((rc = set_lds_limit(fn, lds)) != FRNN_OK) return rc;
   if ((rc = groups_per_launch(p, fn, block, lds, &per_launch)) != FRNN_OK) return rc;
+  if (proj) {
+    const long long tiles = (long long)proj->nrt * proj->nct;
+    const void* fg = proj_overlap_allowed()
+        ? frnn::recurrence_kernel(p.cell, p.mma, p.KS, ktw_class((p.kt_fwd + p.KS - 1) / p.KS, p.NDT), p.NDT, true, true)
+        : nullptr;
+    size_t lds_g = lds;
+    const int nproj = fg ? proj_workers(p, fg, block, tiles, &lds_g) : 0;
+    hipEvent_t t0;
+    const bool timed = allow_timing && timing_begin(st, &t0);
+    if (nproj > 0) {  // one launch: the recurrence's workgroups first, then the projection's
+      a.proj = *proj;
+      a.proj.skip_xcds = proj_skip_xcds(p);
+      // plain (L2-cached) Wx loads, and with them the scouts' L2 prefetch, where
+      // no XCD both writes and reads Wx and every Wx row is whole 128-byte lines
+      a.proj.plain = a.proj.skip_xcds && proj->ncols % 64 == 0 && (reinterpret_cast<uintptr_t>(proj->wx) & 127) == 0;
+      int per_scout = p.ngroups;
+      if (a.proj.plain) use_scouts(p, fg, block, &lds_g, &a.p, &per_scout);
+      if (per_scout < p.ngroups) return FRNN_E_UNSUPPORTED;  // not reached: the scouts keep one launch
+      set_groups(&a.p, 0, p.ngroups);                        // the grid with the scouts' workgroups
+      rc = launch(fg, a.p.grid + nproj, block, lds_g, &a, st);
+      if (timed) timing_end(0, t0, st);
+      return rc;
+    }
+    // a launch of the projection workers alone, then the forward
+    frnn::ProjArgs pa = *proj;
+    rc = launch(frnn::proj_kernel(p.mma), (int)std::min<long long>(4096, (tiles + 3) / 4), 256, 0, &pa, st);
+    if (rc != FRNN_OK) return rc;
+    use_scouts(p, fn, block, &lds, &a.p, &per_launch);
+    rc = launch_groups(&a.p, fn, block, lds, &a, per_launch, st);
+    if (timed) timing_end(0, t0, st);
+    return rc;
+  }
   use_scouts(p, fn, block, &lds, &a.p, &per_launch);
   hipEvent_t t0;
   const bool timed = allow_timing && timing_begin(st, &t0);
@@ -484,6 +566,7 @@ size_t frnn_workspace_bytes(const frnn_desc* d, int which) {
     case 0: return (size_t)p.ws_fwd;
     case 1: return (size_t)p.ws_bwd;
     case 2: return (size_t)p.save_bytes;
+    case 3: return (size_t)proj_ws_bytes(p);
   }
   return 0;
 }
@@ -498,6 +581,36 @@ int frnn_fwd(const frnn_desc* d, const void* wx, const void* R, const void* b, c
   if ((long long)ws_bytes < p.ws_fwd) return FRNN_E_WORKSPACE;
   return fwd_launch(p, wx, R, b, s0, states_out, carry_out, save, static_cast<char*>(ws),
                     static_cast<uint32_t*>(ws), true, reinterpret_cast<hipStream_t>(stream));
+}
+
+int frnn_fwd_projected(const frnn_desc* d, int32_t input_size, const void* x, const void* w_in, void* wx_out,
+                       const void* R, const void* b, const void* s0, void* states_out, void* carry_out, void* save,
+                       void* ws, size_t ws_bytes, frnn_stream_t stream) {
+  Plan p;
+  int rc = make_plan(d, &p);
+  if (rc != FRNN_OK) return rc;
+  if (!x || !w_in || !wx_out || !ws) return FRNN_E_INVALID;
+  if ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(w_in) | reinterpret_cast<uintptr_t>(wx_out)) & 15)
+    return FRNN_E_INVALID;  // 16-byte operand runs
+  if (input_size < 8 || input_size % 8 != 0) return FRNN_E_UNSUPPORTED;
+  if (mma_h16(p.mma) < 0 || p.dt_io != mma_h16(p.mma)) return FRNN_E_UNSUPPORTED;  // 16-bit operands in the MMA type
+  if (p.t0 != 0 || p.Ttot != p.T) return FRNN_E_UNSUPPORTED;                       // whole sequences
+  if ((long long)ws_bytes < proj_ws_bytes(p)) return FRNN_E_WORKSPACE;
+  char* w = static_cast<char*>(ws);
+  frnn::ProjArgs pa;
+  pa.x = x;
+  pa.w = w_in;
+  pa.wx = wx_out;
+  pa.I = input_size;
+  pa.ncols = p.GW * p.N * p.D;
+  pa.B = p.B;
+  pa.T = p.T;
+  pa.nrt = (int)proj_row_tiles(p);
+  pa.nct = (pa.ncols + frnn::kProjCols - 1) / frnn::kProjCols;
+  pa.ready = reinterpret_cast<uint32_t*>(w + p.ws_fwd);
+  pa.next = pa.ready + pa.nrt;
+  return fwd_launch(p, wx_out, R, b, s0, states_out, carry_out, save, w, reinterpret_cast<uint32_t*>(w), true,
+                    reinterpret_cast<hipStream_t>(stream), &pa);
 }
 
 int frnn_fwd_noalloc(const frnn_desc* d, const void* wx, const void* R, const void* b, const void* s0,

@@ -10,31 +10,35 @@
 namespace frnn {
 
 template <int MMA, int KTW, int NDT, int KS>
-static const void* pick(bool fwd) {
-  return fwd ? reinterpret_cast<const void*>(&fwd_kernel<CELL_ELMAN, MMA, KTW, 1, NDT, KS>)
+static const void* pick(bool fwd, bool proj) {
+  // projection-gated forwards (frnn_proj.h): 16-bit operands, one-tile workgroups
+  if constexpr (MMA != MMA_F32 && NDT == 1 && KS <= 4)
+    if (fwd && proj) return reinterpret_cast<const void*>(&fwd_kernel<CELL_ELMAN, MMA, KTW, 1, NDT, KS, true>);
+  if (proj) return nullptr;
+  return fwd ? reinterpret_cast<const void*>(&fwd_kernel<CELL_ELMAN, MMA, KTW, 1, NDT, KS, false>)
              : reinterpret_cast<const void*>(&bwd_kernel<CELL_ELMAN, MMA, KTW, 1, NDT, KS>);
 }
 
 template <int MMA>
-static const void* by_shape(int ks, int ktw, int ndt, bool fwd) {
-  if (ndt == 1 && ks == 1 && ktw == 1) return pick<MMA, 1, 1, 1>(fwd);
-  if (ndt == 1 && ks == 2 && ktw == 1) return pick<MMA, 1, 1, 2>(fwd);
-  if (ndt == 1 && ks == 2 && ktw == 2) return pick<MMA, 2, 1, 2>(fwd);
-  if (ndt == 1 && ks == 4 && ktw == 1) return pick<MMA, 1, 1, 4>(fwd);
-  if (ndt == 1 && ks == 4 && ktw == 2) return pick<MMA, 2, 1, 4>(fwd);
-  if (ndt == 1 && ks == 4 && ktw == 4) return pick<MMA, 4, 1, 4>(fwd);
-  if (ndt == 1 && ks == 8 && ktw == 1) return pick<MMA, 1, 1, 8>(fwd);
-  if (ndt == 1 && ks == 8 && ktw == 2) return pick<MMA, 2, 1, 8>(fwd);
-  if (ndt == 2 && ks == 4 && ktw == 6) return pick<MMA, 6, 2, 4>(fwd);
-  if (ndt == 2 && ks == 4 && ktw == 8) return pick<MMA, 8, 2, 4>(fwd);
+static const void* by_shape(int ks, int ktw, int ndt, bool fwd, bool proj) {
+  if (ndt == 1 && ks == 1 && ktw == 1) return pick<MMA, 1, 1, 1>(fwd, proj);
+  if (ndt == 1 && ks == 2 && ktw == 1) return pick<MMA, 1, 1, 2>(fwd, proj);
+  if (ndt == 1 && ks == 2 && ktw == 2) return pick<MMA, 2, 1, 2>(fwd, proj);
+  if (ndt == 1 && ks == 4 && ktw == 1) return pick<MMA, 1, 1, 4>(fwd, proj);
+  if (ndt == 1 && ks == 4 && ktw == 2) return pick<MMA, 2, 1, 4>(fwd, proj);
+  if (ndt == 1 && ks == 4 && ktw == 4) return pick<MMA, 4, 1, 4>(fwd, proj);
+  if (ndt == 1 && ks == 8 && ktw == 1) return pick<MMA, 1, 1, 8>(fwd, proj);
+  if (ndt == 1 && ks == 8 && ktw == 2) return pick<MMA, 2, 1, 8>(fwd, proj);
+  if (ndt == 2 && ks == 4 && ktw == 6) return pick<MMA, 6, 2, 4>(fwd, proj);
+  if (ndt == 2 && ks == 4 && ktw == 8) return pick<MMA, 8, 2, 4>(fwd, proj);
   return nullptr;
 }
 
-const void* elman_kernel(int mma, int ks, int ktw, int ndt, bool forward) {
+const void* elman_kernel(int mma, int ks, int ktw, int ndt, bool forward, bool proj) {
   switch (mma) {
-    case MMA_BF16: return by_shape<MMA_BF16>(ks, ktw, ndt, forward);
-    case MMA_F16: return by_shape<MMA_F16>(ks, ktw, ndt, forward);
-    case MMA_F32: return by_shape<MMA_F32>(ks, ktw, ndt, forward);
+    case MMA_BF16: return by_shape<MMA_BF16>(ks, ktw, ndt, forward, proj);
+    case MMA_F16: return by_shape<MMA_F16>(ks, ktw, ndt, forward, proj);
+    case MMA_F32: return by_shape<MMA_F32>(ks, ktw, ndt, forward, proj);
   }
   return nullptr;
 }

@@ -7,6 +7,29 @@
 
 namespace frnn {
 
+// Input projection workers (frnn_proj.h): Wx[B][T][ncols] = x[B][T][I] W[ncols][I]^T
+// in 64 x 64 tiles of output rows m = t*B + b and columns.
+constexpr int kProjRows = 64, kProjCols = 64;
+
+struct ProjArgs {
+  const void* x;     // [B][T][I]
+  const void* w;     // [ncols][I]
+  void* wx;          // [B][T][ncols]
+  uint32_t* ready;   // [nrt]: column tiles done per row tile (zeroed before the launch)
+  uint32_t* next;    // tile counter (zeroed before the launch)
+  int I, ncols;      // inner size (multiple of 8), G_W*N*D (multiple of 32)
+  int B, T;
+  int nrt, nct;      // row tiles ceil(B*T/64), column tiles ceil(ncols/64)
+  uint32_t skip_xcds;  // beside the recurrence: XCDs whose workers leave at once (bit per XCD)
+  int plain;           // beside the recurrence: the recurrence reads Wx with plain (L2-cached) loads
+};
+
+// Last row tile that step t of the sequence reads: rows t*B .. t*B+B-1.
+#ifdef __HIPCC__
+__host__ __device__
+#endif
+inline int proj_last_row_tile(int t, int B) { return (int)(((long)(t + 1) * B - 1) / kProjRows); }
+
 struct FwdArgs {
   Plan p;
   const void* wx;
@@ -22,6 +45,7 @@ struct FwdArgs {
   uint32_t* status;
   uint32_t spin_limit;
   unsigned long long* prof;  // phase profile (8 words) or null
+  ProjArgs proj;             // projection-gated launches only: the producers' arguments
 };
 
 struct BwdArgs {
@@ -66,10 +90,11 @@ const void* gemm_dma_kernel(int mma);
 const void* to16_kernel();
 
 // Persistent recurrence kernel for (mma, k-tiles per wave) of one cell; null if not built.
-const void* lstm_kernel(int mma, int ks, int ktw, int ndt, bool forward);
-const void* gru_kernel(int mma, int ks, int ktw, int ndt, bool forward);
-const void* elman_kernel(int mma, int ks, int ktw, int ndt, bool forward);
-const void* slstm_kernel(int mma, int ks, int ktw, int ndt, bool forward);
+// proj: the forward that also runs the input-projection workers (frnn_proj.h).
+const void* lstm_kernel(int mma, int ks, int ktw, int ndt, bool forward, bool proj = false);
+const void* gru_kernel(int mma, int ks, int ktw, int ndt, bool forward, bool proj = false);
+const void* elman_kernel(int mma, int ks, int ktw, int ndt, bool forward, bool proj = false);
+const void* slstm_kernel(int mma, int ks, int ktw, int ndt, bool forward, bool proj = false);
 // LDS floats per hidden-tile team of the persistent kernels (KS compute waves).
 long lstm_lds_floats(bool forward, int ks);
 long gru_lds_floats(bool forward, int ks);
@@ -86,12 +111,12 @@ inline long recurrence_lds_floats(int cell, bool forward, int ks) {
   return 0;
 }
 
-inline const void* recurrence_kernel(int cell, int mma, int ks, int ktw, int ndt, bool forward) {
+inline const void* recurrence_kernel(int cell, int mma, int ks, int ktw, int ndt, bool forward, bool proj = false) {
   switch (cell) {
-    case 0: return lstm_kernel(mma, ks, ktw, ndt, forward);
-    case 1: return gru_kernel(mma, ks, ktw, ndt, forward);
-    case 2: return elman_kernel(mma, ks, ktw, ndt, forward);
-    case 3: return slstm_kernel(mma, ks, ktw, ndt, forward);
+    case 0: return lstm_kernel(mma, ks, ktw, ndt, forward, proj);
+    case 1: return gru_kernel(mma, ks, ktw, ndt, forward, proj);
+    case 2: return elman_kernel(mma, ks, ktw, ndt, forward, proj);
+    case 3: return slstm_kernel(mma, ks, ktw, ndt, forward, proj);
   }
   return nullptr;
 }
@@ -126,6 +151,8 @@ inline long rs_lds_floats(int cell, int ndt) {
 
 // dR GEMM: wide = 64x64 workgroup tiles (4 waves, D % 64 == 0), else 32x32 (1 wave).
 const void* gemm_kernel(int mma, bool wide);
+// Input-projection workers alone (frnn_proj.h), 256 threads: 16-bit MMA types; null otherwise.
+const void* proj_kernel(int mma);
 const void* reduce_kernel();
 const void* zero_kernel();
 

@@ -28,6 +28,7 @@
 #include "frnn_device.h"
 #include "frnn_kernels.h"
 #include "frnn_plan.h"
+#include "frnn_proj.h"
 
 namespace frnn {
 
@@ -512,7 +513,7 @@ template <int CELL, int MMA> struct SaveSize {
 // select. This wave sits close to the step's critical path: each of its LDS
 // bursts (all reads, then all writes or stores) issues without waiting
 // between the accesses.
-template <int CELL, int MMA, int NB, int XS, int OS, int SS>
+template <int CELL, int MMA, int NB, int XS, int OS, int SS, bool PROJ>
 __device__ void fwd_io(const FwdArgs& a, const Team& tm, float* xring, float* ost, float* xf) {
   static_assert(NB == 1, "one 16-row batch tile per group");
   using CS = CellShape<CELL>;
@@ -530,13 +531,48 @@ __device__ void fwd_io(const FwdArgs& a, const Team& tm, float* xring, float* os
   const int lrow = tm.lane >> 2, lquad = tm.lane & 3;
   bool lval;
   const long lbase = wx_dma_index(p, tm.slab, tm.n, tm.dt, tm.lane, 0, 0, XS, &lval);  // + u * wx_t + g * N * D
+  // Projection-gated launches (the launch also runs the input projection, see
+  // frnn_proj.h): before the loads of step u, wait until every row tile that
+  // step reads is complete. The loads are device-coherent (sc1) unless the
+  // host found them safe as plain, L2-cached loads (proj.plain): workers only
+  // on XCDs without groups, and Wx rows that are whole 128-byte lines, so no
+  // line this XCD's L2 fetches holds bytes of a row that is not yet complete
+  // (the kernel's start leaves no stale line in it). The wait walks the row
+  // tiles in order and remembers how far it got. A wait past the spin limit
+  // raises the timeout status and stops waiting (every wave still runs to the end).
+  int ready_rt = 0;
+  bool gave_up = false;
+  auto gate = [&](int u) {
+    if constexpr (PROJ) {
+      const int need = proj_last_row_tile(u, B);
+      uint32_t spins = 0;
+      while (ready_rt <= need && !gave_up) {
+        const uint32_t v = __hip_atomic_load(a.proj.ready + ready_rt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (v >= (uint32_t)a.proj.nct) {
+          ++ready_rt;
+          continue;
+        }
+        __builtin_amdgcn_s_sleep(2);
+        if (++spins >= a.spin_limit) {
+          raise_status(a.status, ST_TIMEOUT);
+          gave_up = true;
+        } else if ((spins & 255u) == 0 && load_status(a.status) != 0) {
+          gave_up = true;
+        }
+      }
+    }
+  };
   auto load_wx = [&](int u) {
+    gate(u);
     float* slot = xring + (long)(u % kFwdRing) * RING;
 #pragma unroll
     for (int g = 0; g < GW; ++g) {
       const char* src = static_cast<const char*>(a.wx) + (lbase + (long)u * wx_t + (long)g * N * D) * XS;
-      if (lval)
-        __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)(slot + g * 256), 16, 0, 0);
+      if (lval) {
+        auto dst = (__attribute__((address_space(3))) void*)(slot + g * 256);
+        if (PROJ && !a.proj.plain) __builtin_amdgcn_global_load_lds(src, dst, 16, 0, 16);
+        else __builtin_amdgcn_global_load_lds(src, dst, 16, 0, 0);
+      }
     }
   };
   // stores: lane -> elements e0 .. e0+3 (four units of one row), from base
@@ -645,7 +681,7 @@ constexpr uint32_t kScoutPatience = 1u << 12;  // polls a scout waits for one st
 // Scout of a group, forward: touches the Wx lines of the group's real batch
 // rows a few steps before the I/O waves load them (see bwd_scout), paced by
 // the hidden-state word member 0 publishes each step.
-template <int CELL, int MMA>
+template <int CELL, int MMA, bool PROJ>
 __device__ void fwd_scout(const FwdArgs& a, const Team& tm, float* lds) {
   constexpr int GW = CellShape<CELL>::GW;
   const Plan& p = a.p;
@@ -669,10 +705,29 @@ __device__ void fwd_scout(const FwdArgs& a, const Team& tm, float* lds) {
                                          __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     return (MMA == MMA_F32 ? w : (w >> 16)) == step_tag(t);
   };
-  for (int u = 3; u < kScoutLead && u < T; ++u) touch(u);
   // patience per step: a scout that loses the pace gives up within ~1 ms
   const uint32_t patience = a.spin_limit < kScoutPatience ? a.spin_limit : kScoutPatience;
   bool live = true;
+  // projection-gated launches (plain loads only): touch step u only once its rows are complete
+  int ready_rt = 0;
+  auto ready = [&](int u) {
+    if constexpr (PROJ) {
+      const int need = proj_last_row_tile(u, B);
+      uint32_t spins = 0;
+      while (live && ready_rt <= need) {
+        if (__hip_atomic_load(a.proj.ready + ready_rt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >=
+            (uint32_t)a.proj.nct) {
+          ++ready_rt;
+          continue;
+        }
+        __builtin_amdgcn_s_sleep(2);
+        if (++spins >= patience) live = false;
+      }
+    }
+    return live;
+  };
+  for (int u = 3; u < kScoutLead && u < T; ++u)
+    if (ready(u)) touch(u);
   for (int j = 0; live && j + kScoutLead < T; ++j) {
     uint32_t spins = 0;
     while (!published(j)) {
@@ -682,12 +737,12 @@ __device__ void fwd_scout(const FwdArgs& a, const Team& tm, float* lds) {
         break;
       }
     }
-    if (live) touch(j + kScoutLead);
+    if (live && ready(j + kScoutLead)) touch(j + kScoutLead);
   }
   __builtin_amdgcn_s_waitcnt(0);
 }
 
-template <int CELL, int MMA, int KTW, int NB, int NDT, int KSC>
+template <int CELL, int MMA, int KTW, int NB, int NDT, int KSC, bool PROJ>
 __global__ void __launch_bounds__(64 * (KSC + 1) * NDT) fwd_kernel(FwdArgs a) {
   using CS = CellShape<CELL>;
   constexpr int GR = CS::GR, GW = CS::GW, GT = CS::GT, S = CS::S;
@@ -696,8 +751,16 @@ __global__ void __launch_bounds__(64 * (KSC + 1) * NDT) fwd_kernel(FwdArgs a) {
   const Plan& p = a.p;
   extern __shared__ float lds[];
   Team tm;
+  if constexpr (PROJ) {
+    if (blockIdx.x >= p.grid) {  // beyond the recurrence's workgroups: input projection
+      // workers on an XCD that hosts recurrence groups leave, so the groups keep
+      // that XCD's L2 to themselves (the host clears every bit when no XCD is free)
+      if (!((a.proj.skip_xcds >> (xcc_id() & 15u)) & 1u)) proj_worker<MMA>(a.proj);
+      return;
+    }
+  }
   if (blockIdx.x >= p.grid - scout_blocks(p)) {  // a scout
-    if (scout_setup(p, tm, a.claim, lds)) fwd_scout<CELL, MMA>(a, tm, lds);
+    if (scout_setup(p, tm, a.claim, lds)) fwd_scout<CELL, MMA, PROJ>(a, tm, lds);
     return;
   }
   if (!team_setup(p, tm, a.claim, a.status, KSC, lds)) return;
@@ -724,9 +787,9 @@ __global__ void __launch_bounds__(64 * (KSC + 1) * NDT) fwd_kernel(FwdArgs a) {
     // saved values: FP16 under the 16-bit policies (sLSTM: FP32), FP32 with FP32 operands
     constexpr int SS = SaveSize<CELL, MMA>::value;
     switch (io_sizes(p.dt_io, p.dt_out)) {
-      case 0: fwd_io<CELL, MMA, NB, 2, 2, SS>(a, tm, xring, ost, xf); break;
-      case 1: fwd_io<CELL, MMA, NB, 2, 4, SS>(a, tm, xring, ost, xf); break;
-      default: fwd_io<CELL, MMA, NB, 4, 4, SS>(a, tm, xring, ost, xf); break;
+      case 0: fwd_io<CELL, MMA, NB, 2, 2, SS, PROJ>(a, tm, xring, ost, xf); break;
+      case 1: fwd_io<CELL, MMA, NB, 2, 4, SS, PROJ>(a, tm, xring, ost, xf); break;
+      default: fwd_io<CELL, MMA, NB, 4, 4, SS, PROJ>(a, tm, xring, ost, xf); break;
     }
     return;
   }

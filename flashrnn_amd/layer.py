@@ -9,20 +9,23 @@ weight ``[G,N,D,I]``, recurrent weight ``[G,N,D,D]``, bias ``[G_T,N,D]``; inputs
 ``[B,T,N,D]`` and the final states ``[S,B,1,N,D]``. ``FlashRNNLayer`` keeps
 that contract on this library's kernels:
 
-* the projection is one library GEMM (hipBLASLt through ``torch.matmul``) of
+* the projection ``Wx[B,T,G,N,D] = x W^T`` runs in the recurrence's own launch
+  (``frnn_fwd_projected``): hand-written MFMA workers on the CUs the
+  recurrence leaves free compute Wx in time order, and the recurrence's I/O
+  waves read each step's rows as soon as they are complete, so the projection
+  costs the forward almost nothing where the recurrence leaves CUs free. Where
+  it does not (the groups fill the GPU) the same workers run in a launch of
+  their own first. 16-bit compute dtypes, head widths that are multiples of 32
+  and input sizes that are multiples of 8 take this path; otherwise (and with
+  ``overlap=False``) the projection is one library GEMM (``torch.matmul``) of
   ``[B*T, I] x [I, G*N*D]``, whose row-major result is already the kernels'
-  ``Wx [B,T,G,N,D]`` layout: nothing is permuted;
+  Wx layout;
 * the recurrence runs with the hidden-state output policy (``FRNN_OUT_HIDDEN``:
   one state written per step) and returns the FP32 carry as the final states;
 * gradients flow to the inputs, the three weights and the initial state; the
   recurrence's follow ``flashrnn_torch`` exactly (also for sLSTM), as
-  ``flashrnn()``'s do;
-* ``chunks`` (a pipeline of the projection of time chunk c+1 on a second
-  stream with the recurrence of chunk c through a step window) is switched
-  off: its first large-batch run on the MI355X (B256 T1024 N8 D128, I1024,
-  four chunks) ended in a GPU memory fault whose cause is not found yet, so
-  that code is taken out and a call with more than one chunk raises
-  ``NotImplementedError``.
+  ``flashrnn()``'s do; ``dx = dWx W`` and ``dW = dWx^T x`` are library GEMMs
+  after the backward recurrence.
 
 Differences from ``TorchLayer``, on purpose: every cell (TorchLayer maps LSTM,
 GRU and Elman onto ``torch.nn`` modules, so it has no sLSTM); one call for all
@@ -35,9 +38,10 @@ from __future__ import annotations
 import torch
 from torch import nn
 
-from .flashrnn import CELL_SIZES, DTYPES
+from . import _lib
+from .flashrnn import _IO, _MMA_OF, CELL_SIZES, DTYPES, _after_call, _drain_pending, _workspace
 from .prepared import KernelConfig, default_config
-from .training import _recurrence
+from .training import _backward, _flags, _recurrence
 
 
 def _check(inputs, input_weight, recurrent, bias, initial, cell):
@@ -60,22 +64,69 @@ def _check(inputs, input_weight, recurrent, bias, initial, cell):
 
 
 def project(inputs, input_weight):
-    """``Wx[B,T,G,N,D] = sum_i x[B,T,i] W[G,N,D,i]``: one GEMM in the operands' dtype."""
+    """``Wx[B,T,G,N,D] = sum_i x[B,T,i] W[G,N,D,i]``: one library GEMM in the operands' dtype."""
     G, N, D, I = input_weight.shape
     B, T, _ = inputs.shape
     return torch.matmul(inputs, input_weight.reshape(G * N * D, I).t()).view(B, T, G, N, D)
 
 
+class _ProjectedRecurrence(torch.autograd.Function):
+    """Projection + recurrence through ``frnn_fwd_projected`` (one launch where the
+    recurrence leaves CUs free); backward: ``frnn_bwd``, then dx and dW as GEMMs."""
+
+    @staticmethod
+    def forward(ctx, x, W, recurrent, bias, initial, cell, config):
+        _drain_pending()
+        lib = _lib.load()
+        B, T, I = x.shape
+        G, N, D, _ = W.shape
+        S = CELL_SIZES[cell][3]
+        dev = x.device
+        training = torch.is_grad_enabled() or any(ctx.needs_input_grad[:5])
+        flags = _flags("hidden", False, cell, config, training, v1=False)
+        d = _lib.FrnnDesc(_lib.CELLS[cell], B, T, N, D, _IO[x.dtype], _lib.FRNN_F32, _MMA_OF[x.dtype], flags,
+                          0.0, 0, 0)
+        s0 = initial[:, :, 0].to(torch.float32).contiguous()
+        wx = torch.empty((B, T, G, N, D), dtype=x.dtype, device=dev)
+        hist = torch.empty((B, T, N, D), dtype=x.dtype, device=dev)
+        carry = torch.empty((S, B, N, D), dtype=torch.float32, device=dev)
+        ws = _workspace(lib.frnn_workspace_bytes(d, 3), dev)
+        save = torch.empty(lib.frnn_workspace_bytes(d, 2), dtype=torch.uint8, device=dev) if training else None
+        stream = torch.cuda.current_stream(dev).cuda_stream
+        rc = lib.frnn_fwd_projected(d, I, x.data_ptr(), W.data_ptr(), wx.data_ptr(), recurrent.data_ptr(),
+                                    bias.data_ptr(), s0.data_ptr(), hist.data_ptr(), carry.data_ptr(),
+                                    save.data_ptr() if save is not None else None, ws.data_ptr(), ws.numel(), stream)
+        _lib.check(rc, "frnn_fwd_projected")
+        _after_call(ws)
+        if training:
+            ctx.save_for_backward(x, W, recurrent, s0, hist, save)
+            ctx.meta = (d, wx.shape, bias.shape, initial.dtype)
+        return hist, carry.unsqueeze(2)
+
+    @staticmethod
+    def backward(ctx, d_out, d_final):
+        x, W, recurrent, s0, hist, save = ctx.saved_tensors
+        d, wshape, bshape, init_dtype = ctx.meta
+        dwx, dR, db, ds0 = _backward(d, recurrent, s0, hist, save, d_out, d_final, wshape, x.dtype, bshape, "hidden")
+        B, T, I = x.shape
+        G, N, D, _ = W.shape
+        dg = dwx.view(B * T, G * N * D)
+        dx = (dg @ W.view(G * N * D, I)).view(B, T, I)
+        dW = (dg.t() @ x.reshape(B * T, I)).view(G, N, D, I)
+        return dx, dW, dR, db, ds0.unsqueeze(2).to(init_dtype), None, None
+
+
 def flashrnn_projected(inputs, input_weight, recurrent, bias, initial=None, cell="lstm", *, dtype="bfloat16",
-                       config=None, chunks=None):
+                       config=None, overlap=True):
     """Projection + recurrence. Returns ``(hidden [B,T,N,D], final [S,B,1,N,D])``;
-    ``final`` is the FP32 carry, ``hidden`` has the compute dtype."""
+    ``final`` is the FP32 carry, ``hidden`` has the compute dtype. ``overlap=False``
+    runs the projection as a library GEMM before the recurrence."""
     _check(inputs, input_weight, recurrent, bias, initial, cell)
     if dtype not in DTYPES:
         raise ValueError(f"dtype {dtype!r} not supported; use one of {tuple(DTYPES)}")
     cdt = DTYPES[dtype]
     S = CELL_SIZES[cell][3]
-    B, T, _ = inputs.shape
+    B, T, I = inputs.shape
     _, N, D, _ = input_weight.shape
     if initial is None:
         initial = torch.zeros((S, B, 1, N, D), dtype=torch.float32, device=inputs.device)
@@ -83,14 +134,10 @@ def flashrnn_projected(inputs, input_weight, recurrent, bias, initial=None, cell
     config = config or default_config(D)
     if not isinstance(config, KernelConfig):
         raise ValueError("config must be a flashrnn_amd.prepared.KernelConfig")
-    grad = torch.is_grad_enabled() and any(t.requires_grad for t in (inputs, input_weight, recurrent, bias, initial))
-    lengths = (T,) if chunks is None else tuple(chunks)
-    if not lengths or any(type(n) is not int or n < 1 for n in lengths) or sum(lengths) != T:
-        raise ValueError("chunk lengths must be positive integers totaling T")
-    if len(lengths) > 1:
-        raise NotImplementedError("the chunked projection pipeline is switched off (an unresolved GPU memory "
-                                  "fault at B256 T1024); call without chunks")
-    # one projection, then the differentiable recurrence (exact gradients)
+    if overlap and cdt != torch.float32 and D % 32 == 0 and D <= 1024 and I % 8 == 0:
+        return _ProjectedRecurrence.apply(x.contiguous(), W.contiguous(), R.contiguous(), b.contiguous(), initial,
+                                          cell, config)
+    # one library projection, then the differentiable recurrence (exact gradients)
     return _recurrence(project(x, W), R, b, initial, cell, "hidden", None, config, v1=False)
 
 
@@ -118,6 +165,6 @@ class FlashRNNLayer(nn.Module):
         self.recurrent = nn.Parameter(recurrent.detach().clone())
         self.bias = nn.Parameter(bias.detach().clone())
 
-    def forward(self, inputs, initial=None, *, chunks=None):
+    def forward(self, inputs, initial=None, *, overlap=True):
         return flashrnn_projected(inputs, self.input_weight, self.recurrent, self.bias, initial, self.cell,
-                                  dtype=self.dtype, config=self.config, chunks=chunks)
+                                  dtype=self.dtype, config=self.config, overlap=overlap)

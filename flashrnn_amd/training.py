@@ -83,35 +83,42 @@ class _Recurrence(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, d_out, d_final):
-        _drain_pending()
-        lib = _lib.load()
         recurrent, s0, hist, save = ctx.saved_tensors
         d, wshape, io, bshape, init_dtype, output_mode = ctx.meta
-        dev = recurrent.device
-        d_carry = d_final[:, :, 0].float().contiguous() if d_final is not None else None
-        d_states = None
-        if d_out is not None:
-            if output_mode == "last":  # the last hidden state is the carry's h (rounded): its cotangent joins d_carry
-                extra = d_out[:, 0].float()
-                if d_carry is None:
-                    d_carry = torch.zeros(s0.shape, dtype=torch.float32, device=dev)
-                d_carry[0] += extra
-            else:
-                d_states = d_out.to(hist.dtype).contiguous()
-        dwx = torch.empty(wshape, dtype=io, device=dev)
-        dR = torch.empty(recurrent.shape, dtype=io, device=dev)
-        db = torch.empty(bshape, dtype=io, device=dev)
-        ds0 = torch.empty(s0.shape, dtype=torch.float32, device=dev)
-        ws = _workspace(lib.frnn_workspace_bytes(d, 1), dev)
-        stream = torch.cuda.current_stream(dev).cuda_stream
-        rc = lib.frnn_bwd(d, recurrent.data_ptr(), s0.data_ptr(), hist.data_ptr(), save.data_ptr(),
-                          d_states.data_ptr() if d_states is not None else None,
-                          d_carry.data_ptr() if d_carry is not None else None,
-                          dwx.data_ptr(), dR.data_ptr(), db.data_ptr(), ds0.data_ptr(), ws.data_ptr(), ws.numel(),
-                          stream)
-        _lib.check(rc, "frnn_bwd")
-        _after_call(ws)
+        dwx, dR, db, ds0 = _backward(d, recurrent, s0, hist, save, d_out, d_final, wshape, io, bshape, output_mode)
         return dwx, dR, db, ds0.unsqueeze(2).to(init_dtype), None, None, None, None, None
+
+
+def _backward(d, recurrent, s0, hist, save, d_out, d_final, wshape, io, bshape, output_mode):
+    """frnn_bwd of a training forward: (dWx, dR, db, ds0 [S,B,N,D] FP32) from the
+    cotangents of its output (``d_out``, per ``output_mode``) and of its FP32 carry."""
+    _drain_pending()
+    lib = _lib.load()
+    dev = recurrent.device
+    d_carry = d_final[:, :, 0].float().contiguous() if d_final is not None else None
+    d_states = None
+    if d_out is not None:
+        if output_mode == "last":  # the last hidden state is the carry's h (rounded): its cotangent joins d_carry
+            extra = d_out[:, 0].float()
+            if d_carry is None:
+                d_carry = torch.zeros(s0.shape, dtype=torch.float32, device=dev)
+            d_carry[0] += extra
+        else:
+            d_states = d_out.to(hist.dtype).contiguous()
+    dwx = torch.empty(wshape, dtype=io, device=dev)
+    dR = torch.empty(recurrent.shape, dtype=io, device=dev)
+    db = torch.empty(bshape, dtype=io, device=dev)
+    ds0 = torch.empty(s0.shape, dtype=torch.float32, device=dev)
+    ws = _workspace(lib.frnn_workspace_bytes(d, 1), dev)
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    rc = lib.frnn_bwd(d, recurrent.data_ptr(), s0.data_ptr(), hist.data_ptr(), save.data_ptr(),
+                      d_states.data_ptr() if d_states is not None else None,
+                      d_carry.data_ptr() if d_carry is not None else None,
+                      dwx.data_ptr(), dR.data_ptr(), db.data_ptr(), ds0.data_ptr(), ws.data_ptr(), ws.numel(),
+                      stream)
+    _lib.check(rc, "frnn_bwd")
+    _after_call(ws)
+    return dwx, dR, db, ds0
 
 
 def recurrence(wx, recurrent, bias, initial, cell="lstm", *, output_mode="hidden", snapshot_dtype=None, config=None,

@@ -26,7 +26,7 @@
  *    the kernels run (a recurrence-exchange timeout, a workgroup placement
  *    that breaks the exchange protocol). frnn_status() reads it.
  *
- * Thread safety: frnn_cell_sizes, frnn_workspace_bytes, frnn_fwd, frnn_bwd,
+ * Thread safety: frnn_cell_sizes, frnn_workspace_bytes, frnn_fwd, frnn_fwd_projected, frnn_bwd,
  * frnn_status and frnn_strerror keep no state between calls and may run from
  * several threads at once; calls that overlap in time must use distinct
  * workspaces. The tuning, test and profiling setters (frnn_set_spin_limit,
@@ -134,7 +134,8 @@ int frnn_cell_sizes(int cell, int32_t* g_r, int32_t* g_w, int32_t* g_t, int32_t*
 
 /* Bytes of the caller-owned areas. which: 0 = forward workspace,
  * 1 = backward workspace, 2 = saved-for-backward area (written by a training
- * forward, read by the matching backward). Returns 0 for an invalid desc. */
+ * forward, read by the matching backward), 3 = workspace of frnn_fwd_projected.
+ * Returns 0 for an invalid desc. */
 size_t frnn_workspace_bytes(const frnn_desc* d, int which);
 
 /* Forward. Replaces FlashRNNFuncFused::forward (fused/flashrnn.cc:257-333).
@@ -145,6 +146,23 @@ size_t frnn_workspace_bytes(const frnn_desc* d, int which);
 int frnn_fwd(const frnn_desc* d, const void* wx, const void* R, const void* b, const void* s0,
              void* states_out, void* carry_out, void* save, void* ws, size_t ws_bytes,
              frnn_stream_t stream);
+
+/* Input projection and forward in one call. Replaces the layer around the reference's
+ * recurrence: TorchLayer (flashrnn/flashrnn2/torch_layer.py:14-80) runs Wx = x W^T as a
+ * separate library GEMM, then the recurrence (README.md:17 leaves the projection to the
+ * caller). Here the projection's workgroups run on the CUs the recurrence leaves free, in
+ * the same launch, and the recurrence reads each step's Wx rows as soon as they are
+ * written; where the recurrence needs the whole GPU (or successive launches) the
+ * projection runs in a launch of its own first. Results equal frnn_fwd on the Wx this
+ * call writes, bitwise, either way.
+ * x [B,T,input_size] and w_in [G_W,N,D,input_size] in dtype_io, which must be the MMA's
+ * 16-bit type (BF16 with FRNN_MMA_BF16, FP16 with FRNN_MMA_F16); input_size a multiple
+ * of 8; x, w_in and wx_out 16-byte aligned. wx_out [B,T,G_W,N,D] (dtype_io) receives
+ * the projection (FP32 accumulation, rounded once). Whole sequences only (no step
+ * window). ws: frnn_workspace_bytes(d, 3) bytes. Other arguments as frnn_fwd. */
+int frnn_fwd_projected(const frnn_desc* d, int32_t input_size, const void* x, const void* w_in, void* wx_out,
+                       const void* R, const void* b, const void* s0, void* states_out, void* carry_out,
+                       void* save, void* ws, size_t ws_bytes, frnn_stream_t stream);
 
 /* Allocation-free forward. No counterpart in the reference: it is for callers that
  * cannot allocate device memory, or have a library do so, around the call -- code under

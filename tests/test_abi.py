@@ -153,6 +153,36 @@ def test_null_pointers_rejected_before_launch(lib):
     assert lib.frnn_status(None, None) == -1
 
 
+def test_projected_workspace_and_validation(lib):
+    """frnn_fwd_projected: its workspace is the forward's plus one counter per 64-row
+    tile of Wx and a tile counter; every argument error returns before a device call
+    (the pointers below are never dereferenced)."""
+    d = desc(B=8, T=1024, N=3, D=256, flags=0)
+    ws_f = lib.frnn_workspace_bytes(ctypes.byref(d), 0)
+    ws_p = lib.frnn_workspace_bytes(ctypes.byref(d), 3)
+    assert ws_p >= ws_f + 4 * (8 * 1024 // 64 + 1)
+    big = 1 << 40
+    ok = [0x10000, 0x20000, 0x30000]  # x, w_in, wx_out: 16-byte aligned stand-ins
+    rest = [0x40000] * 6               # R, b, s0, states, carry, save
+
+    def call(dd, I, ptrs, ws=0x50000, ws_bytes=big):
+        return lib.frnn_fwd_projected(ctypes.byref(dd), I, *ptrs, *rest, ws, ws_bytes, None)
+
+    assert call(d, 64, [None] + ok[1:]) == _lib.FRNN_E_INVALID
+    assert call(d, 64, ok, ws=None) == _lib.FRNN_E_INVALID
+    assert call(d, 64, [ok[0] + 8] + ok[1:]) == _lib.FRNN_E_INVALID        # misaligned x
+    assert call(d, 12, ok) == _lib.FRNN_E_UNSUPPORTED                       # input size not a multiple of 8
+    assert call(d, 0, ok) == _lib.FRNN_E_UNSUPPORTED
+    d32 = desc(B=8, T=64, N=1, D=64, io=_lib.FRNN_F32, mma=_lib.FRNN_MMA_F32, flags=0)
+    assert call(d32, 64, ok) == _lib.FRNN_E_UNSUPPORTED                     # FP32 operands
+    dmix = desc(B=8, T=64, N=1, D=64, io=_lib.FRNN_F16, mma=_lib.FRNN_MMA_BF16, flags=0)
+    assert call(dmix, 64, ok) == _lib.FRNN_E_UNSUPPORTED                    # operands not in the MMA type
+    dwin = _lib.FrnnDesc(_lib.CELLS["lstm"], 8, 32, 1, 64, _lib.FRNN_BF16, _lib.FRNN_F32, _lib.FRNN_MMA_BF16, 0,
+                         0.0, 64, 0)
+    assert call(dwin, 64, ok) == _lib.FRNN_E_UNSUPPORTED                    # a step window
+    assert call(d, 64, ok, ws_bytes=ws_p - 1) == _lib.FRNN_E_WORKSPACE
+
+
 def test_strerror_names_every_code(lib):
     seen = set()
     for code in range(0, -7, -1):

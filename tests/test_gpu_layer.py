@@ -9,8 +9,9 @@ its FP32 projection (from the same BF16 inputs and weights) to BF16 as well.
 Without that, sLSTM gradients that include the final stabilizer m differ at
 elements where the rounding of Wx flips a max(i, log f + m) branch: the exact
 gradient of m jumps there (measured: dW off by 0.95 max-abs-rel; the kernel
-matches the oracle at 3e-3 when both see the same Wx). The pipelined inference
-forward is checked against the same oracle and against the one-chunk forward.
+matches the oracle at 3e-3 when both see the same Wx). BF16 runs both ways of
+computing Wx: the projection workers in the recurrence's launch
+(``frnn_fwd_projected``, the default) and a library GEMM before it.
 """
 
 import pytest
@@ -60,45 +61,23 @@ CASES = [("lstm", 5, 16, 2, 64, 48), ("gru", 3, 12, 2, 96, 64), ("elman", 4, 10,
          ("slstm", 4, 14, 2, 128, 96), ("lstm", 8, 40, 3, 256, 256)]
 
 
-@pytest.mark.parametrize("dtype", ["bfloat16", "float32"])
+@pytest.mark.parametrize("dtype,overlap", [("bfloat16", True), ("bfloat16", False), ("float32", False)],
+                         ids=["bf16-projected", "bf16-library-gemm", "f32"])
 @pytest.mark.parametrize("cell,B,T,N,D,I", CASES, ids=[f"{c[0]}-B{c[1]}T{c[2]}N{c[3]}D{c[4]}I{c[5]}" for c in CASES])
-def test_layer_training(cell, B, T, N, D, I, dtype):
+def test_layer_training(cell, B, T, N, D, I, dtype, overlap):
     from flashrnn_amd import set_strict
     from flashrnn_amd.layer import FlashRNNLayer
 
     set_strict(True)
-    print(f"\n[layer] {cell} B{B} T{T} N{N} D{D} I{I} {dtype}", flush=True)
+    print(f"\n[layer] {cell} B{B} T{T} N{N} D{D} I{I} {dtype} overlap={overlap}", flush=True)
     io = torch.bfloat16 if dtype == "bfloat16" else torch.float32
     cpu, dh, dl = layer_inputs(cell, B, T, N, D, I, seed=62, io=io)
     layer = FlashRNNLayer(*(t.cuda() for t in cpu[1:4]), cell, dtype=dtype)
     x = cpu[0].cuda().requires_grad_()
     s0 = cpu[4].cuda().requires_grad_()
-    h, l = layer(x, s0)
+    h, l = layer(x, s0, overlap=overlap)
     g = torch.autograd.grad((h.float() * dh.cuda()).sum() + (l * dl.cuda()).sum(),
                             (x, layer.input_weight, layer.recurrent, layer.bias, s0))
     torch.cuda.synchronize()
     numerics = "fp32_state_bf16_mma" if dtype == "bfloat16" else "mathematical"
     check((h, l, *g), oracle(cell, cpu, dh, dl, numerics), 1e-2 if dtype == "bfloat16" else 1e-4)
-
-
-@pytest.mark.skip(reason="the chunked projection pipeline is switched off: its first B256 T1024 N8 D128 I1024 "
-                         "run on the MI355X ended in a GPU memory fault whose cause is not found")
-@pytest.mark.parametrize("cell", ["lstm", "slstm", "gru"])
-def test_layer_pipelined_inference(cell):
-    from flashrnn_amd import set_strict
-    from flashrnn_amd.layer import flashrnn_projected
-
-    set_strict(True)
-    print(f"\n[layer] pipelined {cell} B24 T64 N2 D128 I160, chunks 8x8 and 5+27+32", flush=True)
-    cpu, _, _ = layer_inputs(cell, 24, 64, 2, 128, 160, seed=63, io=torch.bfloat16)
-    args = [t.cuda() for t in cpu]
-    with torch.no_grad():
-        h1, l1 = flashrnn_projected(*args, cell)
-        eh, el = flashrnn_layer(*cpu, cell=cell, numerics="fp32_state_bf16_mma", wx_dtype=torch.bfloat16)
-        assert rel(h1, eh) <= 1e-2 and rel(l1, el) <= 1e-2
-        for chunks in ([8] * 8, [5, 27, 32]):
-            h, l = flashrnn_projected(*args, cell, chunks=chunks)  # raises NotImplementedError while switched off
-            torch.cuda.synchronize()
-            # the chunk GEMMs may sum in another order than the whole one: close, not bitwise
-            assert rel(h, h1) <= 2e-3 and rel(l, l1) <= 2e-3, chunks
-            assert rel(h, eh) <= 1e-2 and rel(l, el) <= 1e-2
