@@ -172,17 +172,49 @@ def head_dim_sweep(torch, dev, flashrnn):
     return out
 
 
+def projection_layer(torch, dev, with_backward=True):
+    """The recurrence with its input projection (flashrnn_amd.layer, TorchLayer's contract) at
+    the metric's recurrence, B8 T1024 N3 D256, input size I = N*D = 768, bf16: the projection
+    workers in the recurrence's launch (frnn_fwd_projected) against a library GEMM
+    (torch.matmul, hipBLASLt) before the recurrence, forward and forward+backward."""
+    from flashrnn_amd.layer import flashrnn_projected
+
+    I = N * D
+    g = torch.Generator().manual_seed(7)
+    x = torch.randn(B, T, I, generator=g).to(dev, torch.bfloat16).requires_grad_()
+    W = (torch.randn(G, N, D, I, generator=g) / I**0.5).to(dev, torch.bfloat16).requires_grad_()
+    R = (torch.randn(G, N, D, D, generator=g) / D**0.5).to(dev, torch.bfloat16).requires_grad_()
+    b = (0.1 * torch.randn(G, N, D, generator=g)).to(dev, torch.bfloat16).requires_grad_()
+    dh = torch.randn(B, T, N, D, generator=g).to(dev, torch.bfloat16)
+    out = {"workload": f"LSTM layer B{B} T{T} N{N} D{D} I{I} bf16 (projection + recurrence)"}
+    for name, overlap in (("projection_in_launch", True), ("library_gemm_then_recurrence", False)):
+        def fwd():
+            with torch.no_grad():
+                flashrnn_projected(x, W, R, b, None, "lstm", overlap=overlap)
+
+        def fwdbwd():
+            h, _ = flashrnn_projected(x, W, R, b, None, "lstm", overlap=overlap)
+            torch.autograd.grad(h, (x, W, R, b), grad_outputs=dh)
+
+        out[name] = {"fwd_ms": _time_ms(torch, fwd)}
+        if with_backward:
+            out[name]["fwd_bwd_ms"] = _time_ms(torch, fwdbwd)
+    return out
+
+
 def extras(torch, dev, flashrnn):
     """Side measurements, not the metric:
     * the reference's published head-dimension sweep (v1 cuda_fused LSTM,
       B16 T1024 bf16, H100 SXM; README speed figure head_dim--lstm.svg),
       every (DH, NH) point, forward and forward+backward;
     * FlashRNN2's prepared inference (forward only, hidden-state output,
-      captured HIP graph) at the metric's shape B8 T1024 N3 D256.
+      captured HIP graph) at the metric's shape B8 T1024 N3 D256;
+    * the layer with its input projection at that shape (projection_layer).
     Inputs are seeded normals as in make_inputs."""
     from flashrnn_amd.prepared import PreparedSequence
 
-    out = {"reference_published_sweep": head_dim_sweep(torch, dev, flashrnn)}
+    out = {"reference_published_sweep": head_dim_sweep(torch, dev, flashrnn),
+           "input_projection": projection_layer(torch, dev)}
     g = torch.Generator().manual_seed(7)
     x = torch.randn(B, T, G, N, D, generator=g).to(dev, torch.bfloat16)
     Rp = (torch.randn(G, N, D, D, generator=g) / D**0.5).to(dev, torch.bfloat16)
@@ -252,6 +284,9 @@ def main(argv=None):
     ap.add_argument("--phases", action="store_true", help="also report the in-kernel phase profile")
     ap.add_argument("--trace-out", default=None, help="with --phases: save the per-wave step timelines "
                     "[fwd/bwd][workgroup][wave][step][stamp] (100 MHz clock) as .npy")
+    ap.add_argument("--projection-only", action="store_true",
+                    help="only the forward of the layer-with-input-projection side measurement (one JSON line, "
+                         "not the metric; the command its rocprof summaries were made with)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a plain device copy of MIB MiB (5 times): the reference point that scales "
                          "the FETCH_SIZE / WRITE_SIZE counters to bytes")
@@ -280,6 +315,10 @@ def main(argv=None):
     from flashrnn_amd import _lib, flashrnn, synchronize_and_check
 
     dev = torch.device("cuda", 0)
+    if args.projection_only:
+        print(json.dumps({"input_projection": projection_layer(torch, dev, with_backward=False)}), flush=True)
+        synchronize_and_check()
+        return 0
     (wx, R, b, s0), (dh, dl) = make_inputs(torch, dev)
     leaves = [t.to(dev, torch.bfloat16).requires_grad_() for t in (wx, R, b, s0)]
     dh = dh.to(dev, torch.bfloat16)

@@ -435,7 +435,9 @@ int proj_workers(const Plan& p, const void* fg, int block, long long tiles, size
   // of a free XCD fill its CUs once the recurrence's unused slots there have
   // left. Otherwise the CUs the recurrence leaves, at most one worker wave per tile.
   if (proj_skip_xcds(p)) return cus / frnn::kXcds * frnn::kXcds;
-  const long long useful = (tiles + block / 64 - 1) / (block / 64);
+  // a workgroup per tile where the workgroups compute tiles together, a wave per tile otherwise
+  const int per_wg = block / 64 >= 4 ? 1 : block / 64;
+  const long long useful = (tiles + per_wg - 1) / per_wg;
   return (int)std::min<long long>(free_cus, useful);
 }
 
@@ -497,7 +499,9 @@ int fwd_launch(const Plan& p, const void* wx, const void* R, const void* b, cons
     }
     // a launch of the projection workers alone, then the forward
     frnn::ProjArgs pa = *proj;
-    rc = launch(frnn::proj_kernel(p.mma), (int)std::min<long long>(4096, (tiles + 3) / 4), 256, 0, &pa, st);
+    const void* pk = frnn::proj_kernel(p.mma);
+    if ((rc = set_lds_limit(pk, frnn::proj_lds_bytes())) != FRNN_OK) return rc;
+    rc = launch(pk, (int)std::min<long long>(4096, tiles), 256, frnn::proj_lds_bytes(), &pa, st);
     if (rc != FRNN_OK) return rc;
     use_scouts(p, fn, block, &lds, &a.p, &per_launch);
     rc = launch_groups(&a.p, fn, block, lds, &a, per_launch, st);

@@ -8,8 +8,8 @@
 namespace frnn {
 
 // Input projection workers (frnn_proj.h): Wx[B][T][ncols] = x[B][T][I] W[ncols][I]^T
-// in 64 x 64 tiles of output rows m = t*B + b and columns.
-constexpr int kProjRows = 64, kProjCols = 64;
+// in 128 x 128 tiles of output rows m = t*B + b and columns.
+constexpr int kProjRows = 128, kProjCols = 128;
 
 struct ProjArgs {
   const void* x;     // [B][T][I]
@@ -19,7 +19,7 @@ struct ProjArgs {
   uint32_t* next;    // tile counter (zeroed before the launch)
   int I, ncols;      // inner size (multiple of 8), G_W*N*D (multiple of 32)
   int B, T;
-  int nrt, nct;      // row tiles ceil(B*T/64), column tiles ceil(ncols/64)
+  int nrt, nct;      // row tiles ceil(B*T/128), column tiles ceil(ncols/128)
   uint32_t skip_xcds;  // beside the recurrence: XCDs whose workers leave at once (bit per XCD)
   int plain;           // beside the recurrence: the recurrence reads Wx with plain (L2-cached) loads
 };
@@ -151,8 +151,10 @@ inline long rs_lds_floats(int cell, int ndt) {
 
 // dR GEMM: wide = 64x64 workgroup tiles (4 waves, D % 64 == 0), else 32x32 (1 wave).
 const void* gemm_kernel(int mma, bool wide);
-// Input-projection workers alone (frnn_proj.h), 256 threads: 16-bit MMA types; null otherwise.
+// Input-projection workers alone (frnn_proj.h), 256 threads and proj_lds_bytes() of
+// dynamic LDS: 16-bit MMA types; null otherwise.
 const void* proj_kernel(int mma);
+int proj_lds_bytes();
 const void* reduce_kernel();
 const void* zero_kernel();
 

@@ -8,8 +8,11 @@ namespace frnn {
 
 template <int MMA>
 __global__ void __launch_bounds__(256) proj_alone_kernel(ProjArgs a) {
-  proj_worker<MMA>(a);
+  extern __shared__ float lds[];
+  proj_wg_worker<MMA>(a, reinterpret_cast<char*>(lds));
 }
+
+int proj_lds_bytes() { return kProjLds; }
 
 const void* proj_kernel(int mma) {
   switch (mma) {

@@ -34,6 +34,7 @@ namespace frnn {
 
 constexpr int kFwdRing = 2;   // raw Wx slots in LDS (DMA targets)
 constexpr int kFwdXf = 3;     // converted (FP32) Wx slots in LDS (what the owners read)
+constexpr int kGateBatch = 4;  // projection-readiness counters read per poll
 constexpr int kFwdAhead = 3;  // steps a Wx load goes out ahead of its use
 
 // Backward input pipeline: the I/O wave keeps kBwdRegs iterations of loads in
@@ -547,11 +548,19 @@ __device__ void fwd_io(const FwdArgs& a, const Team& tm, float* xring, float* os
       const int need = proj_last_row_tile(u, B);
       uint32_t spins = 0;
       while (ready_rt <= need && !gave_up) {
-        const uint32_t v = __hip_atomic_load(a.proj.ready + ready_rt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if (v >= (uint32_t)a.proj.nct) {
-          ++ready_rt;
-          continue;
-        }
+        // four counters per poll (each poll waits for this wave's earlier
+        // loads and stores): the wait passes every complete row tile in a row
+        uint32_t v[kGateBatch];
+#pragma unroll
+        for (int k = 0; k < kGateBatch; ++k)
+          v[k] = ready_rt + k < a.proj.nrt
+                     ? __hip_atomic_load(a.proj.ready + ready_rt + k, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                     : 0u;
+        const int before = ready_rt;
+#pragma unroll
+        for (int k = 0; k < kGateBatch; ++k)
+          if (ready_rt == before + k && v[k] >= (uint32_t)a.proj.nct) ++ready_rt;
+        if (ready_rt > before) continue;
         __builtin_amdgcn_s_sleep(2);
         if (++spins >= a.spin_limit) {
           raise_status(a.status, ST_TIMEOUT);
@@ -755,7 +764,10 @@ __global__ void __launch_bounds__(64 * (KSC + 1) * NDT) fwd_kernel(FwdArgs a) {
     if (blockIdx.x >= p.grid) {  // beyond the recurrence's workgroups: input projection
       // workers on an XCD that hosts recurrence groups leave, so the groups keep
       // that XCD's L2 to themselves (the host clears every bit when no XCD is free)
-      if (!((a.proj.skip_xcds >> (xcc_id() & 15u)) & 1u)) proj_worker<MMA>(a.proj);
+      if (!((a.proj.skip_xcds >> (xcc_id() & 15u)) & 1u)) {
+        if constexpr ((KSC + 1) * NDT >= 4) proj_wg_worker<MMA>(a.proj, reinterpret_cast<char*>(lds));
+        else proj_wave_worker<MMA>(a.proj);
+      }
       return;
     }
   }

@@ -161,11 +161,11 @@ class _FusedRecurrence(torch.autograd.Function):
     gradients for Wx, R, b and the initial state."""
 
     @staticmethod
-    def forward(ctx, wx, R, b, s0, cell, mma, opts):
+    def forward(ctx, wx, R, b, s0, cell, mma, opts, grad):
         _drain_pending()
         lib = _lib.load()
         B, T, _, N, D = wx.shape
-        training = torch.is_grad_enabled() or any(ctx.needs_input_grad[:4])
+        training = grad  # a backward can follow (grad mode on at the call, an input requires grad)
         d = _desc(cell, B, T, N, D, wx.dtype, s0.dtype, mma, training, opts)
         dev = wx.device
         S = CELL_SIZES[cell][3]
@@ -210,7 +210,7 @@ class _FusedRecurrence(torch.autograd.Function):
         )
         _lib.check(rc, "frnn_bwd")
         _after_call(ws)
-        return dwx, dR, db, ds0, None, None, None
+        return dwx, dR, db, ds0, None, None, None, None
 
 
 # ----------------------------------------------------------------------- public API
@@ -292,8 +292,9 @@ def flashrnn(
         b = F.pad(b, (0, pad))
         s0 = F.pad(s0, (0, pad))
     opts = (bool(config.gradient_recurrent_cut), config.gradient_recurrent_clipval)
+    grad = torch.is_grad_enabled() and any(t.requires_grad for t in (Wx, R, b, s0))
     hist, carry = _FusedRecurrence.apply(Wx.contiguous(), R.contiguous(), b.contiguous(), s0.contiguous(), cell, mma,
-                                         opts)
+                                         opts, grad)
     if Dp != D:
         hist = hist[..., :D]
         carry = carry[..., :D]

@@ -13,11 +13,11 @@ that contract on this library's kernels:
   (``frnn_fwd_projected``): hand-written MFMA workers on the CUs the
   recurrence leaves free compute Wx in time order, and the recurrence's I/O
   waves read each step's rows as soon as they are complete, so the projection
-  costs the forward almost nothing where the recurrence leaves CUs free. Where
-  it does not (the groups fill the GPU) the same workers run in a launch of
-  their own first. 16-bit compute dtypes, head widths that are multiples of 32
-  and input sizes that are multiples of 8 take this path; otherwise (and with
-  ``overlap=False``) the projection is one library GEMM (``torch.matmul``) of
+  costs the forward almost nothing where the recurrence leaves whole XCDs
+  free. 16-bit compute dtypes, head widths that are multiples of 32 and input
+  sizes that are multiples of 8 can take this path; by default calls without
+  a backward and with fewer than eight head x batch-slab groups do (see
+  ``flashrnn_projected``); otherwise the projection is one library GEMM (``torch.matmul``) of
   ``[B*T, I] x [I, G*N*D]``, whose row-major result is already the kernels'
   Wx layout;
 * the recurrence runs with the hidden-state output policy (``FRNN_OUT_HIDDEN``:
@@ -75,14 +75,14 @@ class _ProjectedRecurrence(torch.autograd.Function):
     recurrence leaves CUs free); backward: ``frnn_bwd``, then dx and dW as GEMMs."""
 
     @staticmethod
-    def forward(ctx, x, W, recurrent, bias, initial, cell, config):
+    def forward(ctx, x, W, recurrent, bias, initial, cell, config, grad):
         _drain_pending()
         lib = _lib.load()
         B, T, I = x.shape
         G, N, D, _ = W.shape
         S = CELL_SIZES[cell][3]
         dev = x.device
-        training = torch.is_grad_enabled() or any(ctx.needs_input_grad[:5])
+        training = grad  # a backward can follow (grad mode on at the call, an input requires grad)
         flags = _flags("hidden", False, cell, config, training, v1=False)
         d = _lib.FrnnDesc(_lib.CELLS[cell], B, T, N, D, _IO[x.dtype], _lib.FRNN_F32, _MMA_OF[x.dtype], flags,
                           0.0, 0, 0)
@@ -113,14 +113,17 @@ class _ProjectedRecurrence(torch.autograd.Function):
         dg = dwx.view(B * T, G * N * D)
         dx = (dg @ W.view(G * N * D, I)).view(B, T, I)
         dW = (dg.t() @ x.reshape(B * T, I)).view(G, N, D, I)
-        return dx, dW, dR, db, ds0.unsqueeze(2).to(init_dtype), None, None
+        return dx, dW, dR, db, ds0.unsqueeze(2).to(init_dtype), None, None, None
 
 
 def flashrnn_projected(inputs, input_weight, recurrent, bias, initial=None, cell="lstm", *, dtype="bfloat16",
-                       config=None, overlap=True):
+                       config=None, overlap=None):
     """Projection + recurrence. Returns ``(hidden [B,T,N,D], final [S,B,1,N,D])``;
-    ``final`` is the FP32 carry, ``hidden`` has the compute dtype. ``overlap=False``
-    runs the projection as a library GEMM before the recurrence."""
+    ``final`` is the FP32 carry, ``hidden`` has the compute dtype. ``overlap``: True runs
+    the projection in the recurrence's launch wherever the kernels allow it, False as a
+    library GEMM before the recurrence, None (default) in the launch where that was
+    measured faster: calls without a backward (no gradient recorded) and fewer than
+    eight head x batch-slab groups."""
     _check(inputs, input_weight, recurrent, bias, initial, cell)
     if dtype not in DTYPES:
         raise ValueError(f"dtype {dtype!r} not supported; use one of {tuple(DTYPES)}")
@@ -134,9 +137,17 @@ def flashrnn_projected(inputs, input_weight, recurrent, bias, initial=None, cell
     config = config or default_config(D)
     if not isinstance(config, KernelConfig):
         raise ValueError("config must be a flashrnn_amd.prepared.KernelConfig")
+    grad = torch.is_grad_enabled() and any(t.requires_grad for t in (x, W, R, b, initial))
+    # The projection's workers pay where the recurrence leaves whole XCDs free (fewer than
+    # eight head x batch-slab groups) and the forward saves nothing for a backward: measured
+    # at B16 T1024 I768, NH*DH = 768, 8% faster than the library GEMM at NH 6 and 7% slower
+    # at NH 12 (every XCD holds groups); at B8 T1024 N3 D256 I768 6% faster without a
+    # backward, 1.5% slower with one (the saved values' stores hold up the readiness polls).
+    if overlap is None:
+        overlap = not grad and N * ((B + 15) // 16) < 8
     if overlap and cdt != torch.float32 and D % 32 == 0 and D <= 1024 and I % 8 == 0:
         return _ProjectedRecurrence.apply(x.contiguous(), W.contiguous(), R.contiguous(), b.contiguous(), initial,
-                                          cell, config)
+                                          cell, config, grad)
     # one library projection, then the differentiable recurrence (exact gradients)
     return _recurrence(project(x, W), R, b, initial, cell, "hidden", None, config, v1=False)
 
@@ -165,6 +176,6 @@ class FlashRNNLayer(nn.Module):
         self.recurrent = nn.Parameter(recurrent.detach().clone())
         self.bias = nn.Parameter(bias.detach().clone())
 
-    def forward(self, inputs, initial=None, *, overlap=True):
+    def forward(self, inputs, initial=None, *, overlap=None):
         return flashrnn_projected(inputs, self.input_weight, self.recurrent, self.bias, initial, self.cell,
                                   dtype=self.dtype, config=self.config, overlap=overlap)

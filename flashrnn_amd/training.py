@@ -53,14 +53,14 @@ def _flags(output_mode, snap32, cell, config, training, v1=True):
 
 class _Recurrence(torch.autograd.Function):
     @staticmethod
-    def forward(ctx, wx, recurrent, bias, initial, cell, output_mode, snapshot_dtype, config, v1=True):
+    def forward(ctx, wx, recurrent, bias, initial, cell, output_mode, snapshot_dtype, config, v1, grad):
         _drain_pending()
         lib = _lib.load()
         B, T, _, N, D = wx.shape
         S = CELL_SIZES[cell][3]
         dev = wx.device
         snap = wx.dtype if snapshot_dtype is None else snapshot_dtype
-        training = torch.is_grad_enabled() or any(ctx.needs_input_grad[:4])
+        training = grad  # a backward can follow (grad mode on at the call, an input requires grad)
         flags = _flags(output_mode, snap == torch.float32 and snap != wx.dtype, cell, config, training, v1)
         mma = _MMA_OF[wx.dtype]
         d = _lib.FrnnDesc(_lib.CELLS[cell], B, T, N, D, _IO[wx.dtype], _lib.FRNN_F32, mma, flags, 0.0, 0, 0)
@@ -86,7 +86,7 @@ class _Recurrence(torch.autograd.Function):
         recurrent, s0, hist, save = ctx.saved_tensors
         d, wshape, io, bshape, init_dtype, output_mode = ctx.meta
         dwx, dR, db, ds0 = _backward(d, recurrent, s0, hist, save, d_out, d_final, wshape, io, bshape, output_mode)
-        return dwx, dR, db, ds0.unsqueeze(2).to(init_dtype), None, None, None, None, None
+        return dwx, dR, db, ds0.unsqueeze(2).to(init_dtype), None, None, None, None, None, None
 
 
 def _backward(d, recurrent, s0, hist, save, d_out, d_final, wshape, io, bshape, output_mode):
@@ -170,7 +170,9 @@ def _recurrence(wx, recurrent, bias, initial, cell, output_mode, snapshot_dtype,
         pad = Dp - D
         args = [F.pad(wx, (0, pad)), F.pad(recurrent, (0, pad, 0, pad)), F.pad(bias, (0, pad)),
                 F.pad(initial, (0, pad))]
-    out, final = _Recurrence.apply(*(t.contiguous() for t in args), cell, output_mode, snapshot_dtype, config, v1)
+    grad = torch.is_grad_enabled() and any(t.requires_grad for t in args)
+    out, final = _Recurrence.apply(*(t.contiguous() for t in args), cell, output_mode, snapshot_dtype, config, v1,
+                                   grad)
     if Dp != D:
         out, final = out[..., :D], final[..., :D]
     return out, final

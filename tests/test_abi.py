@@ -154,13 +154,13 @@ def test_null_pointers_rejected_before_launch(lib):
 
 
 def test_projected_workspace_and_validation(lib):
-    """frnn_fwd_projected: its workspace is the forward's plus one counter per 64-row
-    tile of Wx and a tile counter; every argument error returns before a device call
+    """frnn_fwd_projected: its workspace is the forward's plus one counter per 128-row
+    tile (128 rows) of Wx and a tile counter; every argument error returns before a device call
     (the pointers below are never dereferenced)."""
     d = desc(B=8, T=1024, N=3, D=256, flags=0)
     ws_f = lib.frnn_workspace_bytes(ctypes.byref(d), 0)
     ws_p = lib.frnn_workspace_bytes(ctypes.byref(d), 3)
-    assert ws_p >= ws_f + 4 * (8 * 1024 // 64 + 1)
+    assert ws_p >= ws_f + 4 * (8 * 1024 // 128 + 1)
     big = 1 << 40
     ok = [0x10000, 0x20000, 0x30000]  # x, w_in, wx_out: 16-byte aligned stand-ins
     rest = [0x40000] * 6               # R, b, s0, states, carry, save

@@ -10,9 +10,10 @@ FP32 GEMM of the same 16-bit operands.
   that Wx, and the overlapped launch bitwise equal to the separate one.
 
 Cases: the LSTM at the C2 head shape (B8 N3 D256, 48 recurrence CUs), ragged
-batch and time, widths and input sizes that leave partial 64-wide tiles
-(I = 8, 40, 136), FP16 operands, and a recurrence that fills every CU (the
-workers then run in their own launch). The layer at C2 (T1024, I768) is
+batch and time, widths and input sizes that leave partial tiles (I = 8, 40,
+136; 32 and 576 columns), workers in workgroups of two, three, five and
+eight waves (D = 32, 64, 256, 768), FP16 operands, and a recurrence that
+fills every CU (the workers then run in their own launch). The layer at C2 (T1024, I768) is
 checked forward and backward against the oracle's projection + flashrnn_torch.
 """
 
@@ -86,6 +87,8 @@ CASES = [
     ("elman", 3, 17, 1, 32, 8, torch.bfloat16, True),
     ("slstm", 16, 20, 2, 128, 64, torch.bfloat16, False),
     ("lstm", 24, 50, 2, 64, 136, torch.float16, True),
+    ("gru", 16, 40, 1, 768, 256, torch.bfloat16, True),    # two-tile workgroups (eight waves)
+    ("lstm", 8, 30, 1, 640, 128, torch.float16, False),
     ("lstm", 128, 16, 4, 128, 64, torch.bfloat16, False),  # 256 recurrence workgroups: a separate launch
 ]
 
@@ -130,7 +133,7 @@ def test_c2_layer_training():
     layer = FlashRNNLayer(*(t.cuda() for t in cpu[1:4]), "lstm", dtype="bfloat16")
     x = cpu[0].cuda().requires_grad_()
     s0 = cpu[4].cuda().requires_grad_()
-    h, l = layer(x, s0)
+    h, l = layer(x, s0, overlap=True)  # the projection in the recurrence's launch, also with a backward
     g = torch.autograd.grad((h.float() * dh.cuda()).sum() + (l * dl.cuda()).sum(),
                             (x, layer.input_weight, layer.recurrent, layer.bias, s0))
     torch.cuda.synchronize()
