@@ -47,14 +47,15 @@ def inputs(cell, B, T, N, D, I, io, seed):
     return [t.to(io).cuda() for t in (x, W, R, b)] + [s0.cuda()]
 
 
-def forward(cell, B, T, N, D, I, io, args, *, projected, overlap=True, training=False, wx_in=None):
+def forward(cell, B, T, N, D, I, io, args, *, projected, overlap=True, training=False, wx_in=None, flags=None):
     lib = _lib.load()
     gr, gw, gt, S = CELL_SIZES[cell]
     x, W, R, b, s0 = args
-    flags = _lib.FRNN_OUT_HIDDEN | (_lib.FRNN_TRAINING if training else 0)
+    full = flags is not None and not (flags & _lib.FRNN_OUT_HIDDEN)
+    flags = (_lib.FRNN_OUT_HIDDEN if flags is None else flags) | (_lib.FRNN_TRAINING if training else 0)
     d = _lib.FrnnDesc(_lib.CELLS[cell], B, T, N, D, IO[io], _lib.FRNN_F32, MMA[io], flags, 0.0, 0, 0)
     wx = torch.empty((B, T, gw, N, D), dtype=io, device="cuda") if projected else wx_in
-    hist = torch.empty((B, T, N, D), dtype=io, device="cuda")
+    hist = torch.empty((S, B, T, N, D) if full else (B, T, N, D), dtype=io, device="cuda")
     carry = torch.empty((S, B, N, D), dtype=torch.float32, device="cuda")
     ws = torch.zeros(lib.frnn_workspace_bytes(ctypes.byref(d), 3 if projected else 0), dtype=torch.uint8,
                      device="cuda")
@@ -138,3 +139,21 @@ def test_c2_layer_training():
                             (x, layer.input_weight, layer.recurrent, layer.bias, s0))
     torch.cuda.synchronize()
     check((h, l, *g), oracle("lstm", cpu, dh, dl, "fp32_state_bf16_mma"), 1e-2)
+
+
+@pytest.mark.parametrize("mode", ["shared-exchange", "full-states"])
+def test_projected_options(mode):
+    """The placement-free exchange (FRNN_XCD_SHARED: device-coherent Wx loads, no
+    scouts) and the full-state output policy, LSTM B8 T48 N3 D256 I256: bitwise
+    equal to frnn_fwd on the Wx the call wrote, and to the workers' own launch."""
+    print(f"\n[projected] {mode}", flush=True)
+    cell, B, T, N, D, I, io = "lstm", 8, 48, 3, 256, 256, torch.bfloat16
+    flags = (_lib.FRNN_OUT_HIDDEN | _lib.FRNN_XCD_SHARED) if mode == "shared-exchange" else 0
+    args = inputs(cell, B, T, N, D, I, io, seed=72)
+    wx, hist, carry, _ = forward(cell, B, T, N, D, I, io, args, projected=True, flags=flags)
+    wx1, hist1, carry1, _ = forward(cell, B, T, N, D, I, io, args, projected=True, overlap=False, flags=flags)
+    _, hist2, carry2, _ = forward(cell, B, T, N, D, I, io, args, projected=False, wx_in=wx, flags=flags)
+    torch.cuda.synchronize()
+    assert torch.equal(wx, wx1)
+    assert torch.equal(hist, hist1) and torch.equal(carry, carry1)
+    assert torch.equal(hist, hist2) and torch.equal(carry, carry2)
