@@ -30,6 +30,21 @@ __host__ __device__
 #endif
 inline int proj_last_row_tile(int t, int B) { return (int)(((long)(t + 1) * B - 1) / kProjRows); }
 
+// Element indices the projection workers address (frnn_proj.h), shared with
+// the host bounds check (tests/bounds/proj_bounds.cpp). Rows past B*T read x
+// row 0 and columns past ncols read W row 0 (their products are never
+// stored); an 8-run whose k lies past I reads k 0 of its row instead (masked
+// out of the products), so every address stays inside its operand.
+FRNN_HD inline long proj_x_row(const ProjArgs& pa, long m) {
+  const long rows = (long)pa.B * pa.T, mm = m < rows ? m : 0;
+  return ((mm % pa.B) * pa.T + mm / pa.B) * pa.I;
+}
+FRNN_HD inline long proj_w_row(const ProjArgs& pa, int c) { return (long)(c < pa.ncols ? c : 0) * pa.I; }
+FRNN_HD inline int proj_k8(const ProjArgs& pa, int k8) { return k8 < pa.I ? k8 : 0; }
+FRNN_HD inline long proj_wx_elem(const ProjArgs& pa, long m, int c) {
+  return ((m % pa.B) * pa.T + m / pa.B) * pa.ncols + c;
+}
+
 struct FwdArgs {
   Plan p;
   const void* wx;

@@ -51,8 +51,6 @@ __device__ __forceinline__ void proj_store(const ProjArgs& pa, const f32x4 (&acc
   for (int j = 0; j < 4; ++j) {
     const long m = m0 + 16 * j + r16;
     if (m >= rows) continue;
-    const long t = m / pa.B, b = m % pa.B;
-    const long row = (b * pa.T + t) * pa.ncols;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int c = c0 + 16 * i + 4 * kq;
@@ -61,17 +59,9 @@ __device__ __forceinline__ void proj_store(const ProjArgs& pa, const f32x4 (&acc
                                    ((unsigned long long)op_bits<MMA>(acc[i][j][1]) << 16) |
                                    ((unsigned long long)op_bits<MMA>(acc[i][j][2]) << 32) |
                                    ((unsigned long long)op_bits<MMA>(acc[i][j][3]) << 48);
-      __hip_atomic_store(wx + (row + c) / 4, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(wx + proj_wx_elem(pa, m, c) / 4, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   }
-}
-
-// x row of output row m (t = m / B, b = m % B); row 0 for rows past the end
-// (their products are never stored).
-__device__ __forceinline__ const unsigned short* proj_xrow(const ProjArgs& pa, long m) {
-  const long rows = (long)pa.B * pa.T;
-  const long mm = m < rows ? m : 0;
-  return static_cast<const unsigned short*>(pa.x) + ((mm % pa.B) * pa.T + mm / pa.B) * pa.I;
 }
 
 // Take the next tile: every lane of the calling wave takes part (lane 0 adds
@@ -101,15 +91,15 @@ __device__ void proj_wave_worker(const ProjArgs& pa) {
     for (int quarter = 0; quarter < 4; ++quarter) {
       const int c0 = ct * kProjCols + 64 * (quarter & 1);
       const long m0 = (long)rt * kProjRows + 64 * (quarter >> 1);
+      const unsigned short* x = static_cast<const unsigned short*>(pa.x);
       const unsigned short* ap[4];
       const unsigned short* bp[4];
       bool av[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const int c = c0 + 16 * i + r16;
-        av[i] = c < pa.ncols;
-        ap[i] = w + (long)(av[i] ? c : 0) * pa.I + 8 * kq;
-        bp[i] = proj_xrow(pa, m0 + 16 * i + r16) + 8 * kq;
+        av[i] = c0 + 16 * i + r16 < pa.ncols;
+        ap[i] = w + proj_w_row(pa, c0 + 16 * i + r16);
+        bp[i] = x + proj_x_row(pa, m0 + 16 * i + r16);
       }
       f32x4 acc[4][4];
 #pragma unroll
@@ -118,13 +108,13 @@ __device__ void proj_wave_worker(const ProjArgs& pa) {
         for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
       Frag<MMA> fa0[4], fb0[4], fa1[4], fb1[4];
       auto load = [&](Frag<MMA>* fa, Frag<MMA>* fb, int k0) {
-        // k beyond I: zeros, from an address kept inside the operand
+        // k beyond I: zeros (the address stays inside the operand)
         const bool kin = k0 + 8 * kq < pa.I;
-        const int kk = kin ? k0 : 0;
+        const int k8 = proj_k8(pa, k0 + 8 * kq);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          proj_load<MMA>(fa[i], ap[i] + kk, kin && av[i]);
-          proj_load<MMA>(fb[i], bp[i] + kk, kin);
+          proj_load<MMA>(fa[i], ap[i] + k8, kin && av[i]);
+          proj_load<MMA>(fb[i], bp[i] + k8, kin);
         }
       };
       auto step = [&](const Frag<MMA>* fa, const Frag<MMA>* fb) {
@@ -189,6 +179,7 @@ __device__ void proj_wg_worker(const ProjArgs& pa, char* lds) {
     const int rt = tile / pa.nct, ct = tile % pa.nct;
     const int c0 = ct * kProjCols;
     const long m0 = (long)rt * kProjRows;
+    const unsigned short* x = static_cast<const unsigned short*>(pa.x);
     const unsigned short* asrc[4];
     const unsigned short* bsrc[4];
     int qlog[4];
@@ -196,19 +187,18 @@ __device__ void proj_wg_worker(const ProjArgs& pa, char* lds) {
     for (int j = 0; j < 4; ++j) {
       const int r = wv * 32 + 8 * j + lrow;
       qlog[j] = (lpos ^ (r >> 1)) & 7;
-      const int c = c0 + r;
-      asrc[j] = w + (long)(c < pa.ncols ? c : 0) * pa.I + 8 * qlog[j];
-      bsrc[j] = proj_xrow(pa, m0 + r) + 8 * qlog[j];
+      asrc[j] = w + proj_w_row(pa, c0 + r);
+      bsrc[j] = x + proj_x_row(pa, m0 + r);
     }
     auto issue = [&](int k0) {
       char* st = lds + (k0 / 64 & 1) * kProjStage;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        // k beyond I: read k 0 of the row instead (masked out of the products)
-        const int kk = k0 + 8 * qlog[j] < pa.I ? k0 : -8 * qlog[j];
-        __builtin_amdgcn_global_load_lds(asrc[j] + kk, (__attribute__((address_space(3))) void*)(st + (wv * 32 + 8 * j) * 128),
+        const int k8 = proj_k8(pa, k0 + 8 * qlog[j]);
+        __builtin_amdgcn_global_load_lds(asrc[j] + k8,
+                                         (__attribute__((address_space(3))) void*)(st + (wv * 32 + 8 * j) * 128),
                                          16, 0, 0);
-        __builtin_amdgcn_global_load_lds(bsrc[j] + kk,
+        __builtin_amdgcn_global_load_lds(bsrc[j] + k8,
                                          (__attribute__((address_space(3))) void*)(st + 128 * 128 + (wv * 32 + 8 * j) * 128),
                                          16, 0, 0);
       }

@@ -7,6 +7,11 @@ each against its buffer's extent. The cases include the shape of the
 chunked-projection run that ended in a GPU memory fault (B256 T1024 N8 D128,
 Wx = 2^30 elements = 2 GiB in BF16, four step windows of 256), unchunked and
 in the full-state and training policies, and the other configurations.
+
+tests/bounds/proj_bounds.cpp does the same for the input projection's workers
+(frnn_fwd_projected): every operand load of both worker kinds, including the
+k runs past the input size and the rows / columns past the end, every Wx
+store, the readiness counters and the forward's gate reads.
 """
 
 import pathlib
@@ -61,3 +66,37 @@ def test_forward_addressing_in_bounds(checker, case):
     res = subprocess.run([str(checker), *map(str, case)], capture_output=True, text=True, timeout=300)
     assert res.returncode == 0, res.stdout[-3000:] + res.stderr[-2000:]
     assert res.stdout.strip().endswith("violations 0")
+
+
+PROJ_SRC = ROOT / "tests" / "bounds" / "proj_bounds.cpp"
+PROJ_CASES = [
+    # cell, B, T, N, D, io, I
+    (LSTM, 8, 1024, 3, 256, BF16, 768),    # the layer at C2
+    (GRU, 5, 33, 2, 96, BF16, 40),         # ragged rows and k, 576 columns
+    (ELMAN, 3, 17, 1, 32, BF16, 8),        # one partial column tile, I = 8
+    (LSTM, 24, 50, 2, 64, 2, 136),         # FP16
+    (GRU, 16, 40, 1, 768, BF16, 256),
+    (LSTM, 256, 64, 8, 128, BF16, 1024),   # wide input, many row tiles
+]
+
+
+@pytest.fixture(scope="module")
+def proj_checker(tmp_path_factory):
+    if not _lib.LIB_PATH.exists():
+        pytest.skip("libfrnn.so is not built (python -m flashrnn_amd.build)")
+    gxx = shutil.which("g++")
+    if gxx is None:
+        pytest.skip("g++ not found")
+    exe = tmp_path_factory.mktemp("bounds") / "proj_bounds"
+    lib_dir = str(_lib.LIB_PATH.parent)
+    subprocess.run([gxx, "-O2", "-std=c++17", str(PROJ_SRC), "-o", str(exe), f"-L{lib_dir}", "-lfrnn",
+                    f"-Wl,-rpath,{lib_dir}"], check=True)
+    return exe
+
+
+@pytest.mark.parametrize("case", PROJ_CASES, ids=["cell{}-B{}T{}N{}D{}-io{}-I{}".format(*c) for c in PROJ_CASES])
+def test_projection_addressing_in_bounds(proj_checker, case):
+    res = subprocess.run([str(proj_checker), *map(str, case)], capture_output=True, text=True, timeout=300)
+    print(res.stdout)
+    assert res.returncode == 0, res.stdout + res.stderr
+    assert "violations 0" in res.stdout
