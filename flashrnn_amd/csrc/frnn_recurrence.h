@@ -80,7 +80,7 @@ struct Lds {
     return 2L * KS * NB * RED_F + (long)kFwdRing * RING + 2L * NV * NE + (long)kFwdXf * XF;
   }
   __host__ __device__ static constexpr long bwd(int KS) {
-    return 2L * NB * KS * RED_B + (long)kBwdStage * NE * NV + 2L * NE * NOB;
+    return 2L * NB * KS * RED_B + (long)kBwdStage * NE * NV + 2L * NE * NOB + 16;  // + the owners' step flags
   }
 };
 
@@ -1282,6 +1282,9 @@ __global__ void __launch_bounds__(64 * (KSC + 1) * NDT) bwd_kernel(BwdArgs a) {
   float* red = lds + tm.team * Lds<CELL, NB>::bwd(KS);  // [2][NB][KS][304]
   float* iring = red + 2L * NB * KS * RED_B;             // [3][NIN][NE]
   float* ost = iring + (long)kBwdStage * NIN * NE;       // [2][NOB][NE]
+  // [owner wave]: last step it published (an LDS pointer: generic atomics would be flat operations)
+  __attribute__((address_space(3))) uint32_t* pubf =
+      (__attribute__((address_space(3))) uint32_t*)reinterpret_cast<uint32_t*>(ost + 2L * NOB * NE);
 
   if (tm.kw == KS) {
     // saved values: FP16 under the 16-bit policies (sLSTM: FP32), FP32 with FP32 operands
@@ -1367,8 +1370,18 @@ __global__ void __launch_bounds__(64 * (KSC + 1) * NDT) bwd_kernel(BwdArgs a) {
 
   Prof prof;
   prof.init(a.prof != nullptr && blockIdx.x == 0, a.prof != nullptr);
+  // Waves that own no element (KS > 4) start their poll late: polled at the
+  // loop head, the exchange is stale, and the re-polls hold the CU's in-order
+  // memory returns and the SIMDs the owners' pointwise runs on. Measured (LSTM
+  // backward): with at most 8 batch rows (paired polls) a fixed delay of ~500
+  // cycles is best (C2 1.61 -> 1.52 ms; waiting for the owners' flag in LDS
+  // 1.58 ms); with 16 rows waiting for the owners' flag, checked every ~250
+  // cycles, is (B16 N2 D384 3.81 -> 3.43 ms, N1 D512 4.53 -> 4.22 ms; the fixed
+  // delay 3.59 and 4.28 ms).
+  constexpr int kOwnerWaves = (NE + 63) / 64 < KS ? (NE + 63) / 64 : KS;
+  if (tm.kw == 0 && tm.lane < kOwnerWaves) pubf[tm.lane] = 0u;
   __builtin_amdgcn_s_waitcnt(0);  // no set-up load pending at the loop head (see the forward kernel)
-  lds_barrier();  // inputs of iterations 0 and 1 staged by the I/O wave
+  lds_barrier();  // inputs of iterations 0 and 1 staged by the I/O wave; the flags clear
   // One-tile workgroups read the owners' inputs of the next iteration from LDS
   // during this iteration's poll (the I/O wave staged them before the previous
   // barrier), so no LDS read stands between the loop head and the pointwise
@@ -1444,6 +1457,9 @@ __global__ void __launch_bounds__(64 * (KSC + 1) * NDT) bwd_kernel(BwdArgs a) {
       for (int g = 0; g < GW; ++g) os[g * NE + e] = dwx[g];
       if constexpr (CELL == CELL_GRU) os[3 * NE + e] = dry[0];
     }
+    if constexpr (KS > kOwnerWaves)
+      if (!pair && tm.kw < kOwnerWaves && tm.lane == 0)  // (the paired polls wait a fixed delay instead)
+        __hip_atomic_store(pubf + tm.kw, (uint32_t)it + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
     prof.mark(3);
     prof.stamp(it, 1);
 
@@ -1462,6 +1478,23 @@ __global__ void __launch_bounds__(64 * (KSC + 1) * NDT) bwd_kernel(BwdArgs a) {
       if constexpr (kPrefetch)
         if (it + 1 < T) read_in(it + 1, in_next);
     };
+    if constexpr (KS > kOwnerWaves) {
+      if (tm.kw >= kOwnerWaves && !cut) {
+        if (pair) {
+          __builtin_amdgcn_s_sleep(8);
+        } else {
+          // bounded: the owners raise their flags every iteration
+          for (uint32_t w = 0; w < (1u << 20); ++w) {
+            bool pub = true;
+#pragma unroll
+            for (int k = 0; k < kOwnerWaves; ++k)
+              pub &= __hip_atomic_load(pubf + k, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) > (uint32_t)it;
+            if (pub) break;
+            __builtin_amdgcn_s_sleep(4);
+          }
+        }
+      }
+    }
     if (cut) {  // gradient_recurrent_cut: no R^T dG reaches h_{t-1}
       zero();
       between();
