@@ -294,7 +294,7 @@ def main(argv=None):
     if args.gpus != 1:
         print(
             f"bench.py measures one GPU only: the recurrence shards over heads/batch with no per-step "
-            f"exchange), and this build runs on single-GPU boxes; got --gpus {args.gpus}",
+            f"exchange, and this build runs on single-GPU boxes; got --gpus {args.gpus}",
             file=sys.stderr,
         )
         return 2
