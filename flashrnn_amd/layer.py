@@ -142,7 +142,7 @@ def flashrnn_projected(inputs, input_weight, recurrent, bias, initial=None, cell
     # eight head x batch-slab groups) and the forward saves nothing for a backward: measured
     # at B16 T1024 I768, NH*DH = 768, 8% faster than the library GEMM at NH 6 and 7% slower
     # at NH 12 (every XCD holds groups); at B8 T1024 N3 D256 I768 6% faster without a
-    # backward, 1.5% slower with one (the saved values' stores hold up the readiness polls).
+    # backward, 1.5% slower with one.
     if overlap is None:
         overlap = not grad and N * ((B + 15) // 16) < 8
     if overlap and cdt != torch.float32 and D % 32 == 0 and D <= 1024 and I % 8 == 0:
