@@ -207,13 +207,19 @@ int make_plan(const frnn_desc* d, Plan* p) {
   // width with an even tile count (half the workgroups per group)
   if (const char* e = std::getenv("FRNN_NDT"))
     if (std::atoi(e) == 2 && (p->D / 16) % 2 == 0) p->NDT = 2;
-  // contraction split (compute waves per hidden tile, plus one I/O wave): forward
-  // up to 4; backward up to 8 where D/32 >= 8 (its exchange operand is GR times
-  // wider, so splitting it further shortens each wave's poll). Two-tile
+  // contraction split (compute waves per hidden tile, plus one I/O wave):
+  // forward 4 (two-tile workgroups: up to 4); backward up to 8 where D/32 >= 8
+  // (its exchange operand is GR times wider, so splitting it further shortens
+  // each wave's poll). Two-tile
   // workgroups whose resident R slice does not fit beside 4 waves per tile use 3
   // (8 waves: two per SIMD, 256 registers each). FRNN_KS / FRNN_KS_BWD
   // (environment, read per plan) override within the built set.
-  p->KS = KT >= 4 ? 4 : (KT >= 2 ? 2 : 1);
+  // One-tile workgroups take four compute waves also where D/32 < 4: the
+  // waves without k-tiles poll nothing and add a zero partial, and the 256
+  // elements of the tile are spread one per lane instead of 2-4 (measured at
+  // B16 T1024: D32 forward 1.43 -> 1.17 ms, D64 1.23 -> 1.19 ms).
+  p->KS = (KT >= 4 || p->NDT == 1) ? 4 : (KT >= 2 ? 2 : 1);
+  if (p->NDT == 1 && KT < 4 && !fits(*p, 4, true)) p->KS = KT >= 2 ? 2 : 1;
   if (p->NDT == 2 && !fits(*p, 4, true)) p->KS = 3;
   p->KSB = (KT >= 8 && p->NDT == 1) ? 8 : p->KS;
   if (p->NDT == 1 && p->KSB == 8 && !fits(*p, 8, false)) p->KSB = 4;
@@ -221,7 +227,8 @@ int make_plan(const frnn_desc* d, Plan* p) {
   auto ks_env = [&](const char* name, int* ks) {
     if (const char* e = std::getenv(name)) {
       const int v = std::atoi(e);
-      if ((v == 1 || v == 2 || v == 4 || (v == 8 && p->NDT == 1) || (v == 3 && p->NDT == 2)) && v <= KT) *ks = v;
+      if ((v == 1 || v == 2 || v == 4 || (v == 8 && p->NDT == 1) || (v == 3 && p->NDT == 2)) && (v <= KT || v <= 4))
+        *ks = v;
     }
   };
   ks_env("FRNN_KS", &p->KS);

@@ -264,6 +264,15 @@ __device__ __forceinline__ uint32_t gather_mma(const Xchg& x, const int (&word)[
   bool first = true;
   using Op = Operand<MMA, SPLIT>;
   uint32_t spins = 0;
+  // A wave with no k-tiles (more compute waves than k-tiles: only where each
+  // wave has at most one, NF == 1) polls nothing but still does its between-work.
+  if constexpr (NF == 1) {
+    if (nf <= 0) {
+      zero();
+      between();
+      return 0;
+    }
+  }
   if constexpr (NF <= PollChunk<MMA, NDT>::value && SPEC) {
     while (true) {
       zero();
@@ -437,6 +446,15 @@ __device__ __forceinline__ uint32_t gather_pair_mma(const Xchg& x, const int (&w
   // speculative: one chunk, multiplied while its tags are checked; otherwise
   // each chunk is multiplied once all of its tags are fresh
   constexpr bool kSpec = SPEC && NP <= PollChunk<MMA, NDT>::value;
+  // A wave with no k-tiles (more compute waves than k-tiles: only where each
+  // wave has at most one, NF == 1) polls nothing but still does its between-work.
+  if constexpr (NF == 1) {
+    if (nf <= 0) {
+      zero();
+      between();
+      return 0;
+    }
+  }
   const int hi = (threadIdx.x >> 3) & 1;  // lane % 16 >= 8
   // the pair's products: the even tile in place, the odd one moved down 8 lanes
   auto pair_prod = [&](Op o, int i) {
