@@ -221,7 +221,9 @@ int make_plan(const frnn_desc* d, Plan* p) {
   p->KS = (KT >= 4 || p->NDT == 1) ? 4 : (KT >= 2 ? 2 : 1);
   if (p->NDT == 1 && KT < 4 && !fits(*p, 4, true)) p->KS = KT >= 2 ? 2 : 1;
   if (p->NDT == 2 && !fits(*p, 4, true)) p->KS = 3;
-  p->KSB = (KT >= 8 && p->NDT == 1) ? 8 : p->KS;
+  // (also where the backward's operand alone is wide: G_R*D/32 >= 16, LSTM
+  // B16 T1024 D128 backward 1.86 -> 1.54 ms; at D64, 8 k-tiles, it was slower)
+  p->KSB = ((KT >= 8 || p->kt_bwd >= 16) && p->NDT == 1) ? 8 : p->KS;
   if (p->NDT == 1 && p->KSB == 8 && !fits(*p, 8, false)) p->KSB = 4;
   if (p->NDT == 2 && !fits(*p, p->KSB, false)) p->KSB = 3;
   auto ks_env = [&](const char* name, int* ks) {
