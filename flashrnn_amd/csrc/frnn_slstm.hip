@@ -12,7 +12,7 @@ namespace frnn {
 template <int MMA, int KTW, int NDT, int KS>
 static const void* pick(bool fwd, bool proj) {
   // projection-gated forwards (frnn_proj.h): 16-bit operands
-  if constexpr (MMA != MMA_F32 && KS <= 4)
+  if constexpr (MMA != MMA_F32)
     if (fwd && proj) return reinterpret_cast<const void*>(&fwd_kernel<CELL_SLSTM, MMA, KTW, 1, NDT, KS, true>);
   if (proj) return nullptr;
   return fwd ? reinterpret_cast<const void*>(&fwd_kernel<CELL_SLSTM, MMA, KTW, 1, NDT, KS, false>)

@@ -73,6 +73,13 @@ CASES = [
     ("slstm", 16, 32, 4, 192),
     ("lstm", 8, 12, 1, 640),
     ("slstm", 5, 8, 1, 576),
+    # planner classes: 8 forward waves (D >= 512), 8 backward waves from a wide
+    # backward operand (G_R*D/32 >= 16, D128), 4 forward waves at D/32 < 4 (D96)
+    ("lstm", 5, 9, 1, 512),
+    ("gru", 12, 10, 2, 512),
+    ("lstm", 16, 11, 2, 128),
+    ("slstm", 4, 9, 2, 128),
+    ("gru", 9, 8, 2, 96),
 ]
 
 
