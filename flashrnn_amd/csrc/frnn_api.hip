@@ -219,9 +219,12 @@ int make_plan(const frnn_desc* d, Plan* p) {
   // elements of the tile are spread one per lane instead of 2-4 (measured at
   // B16 T1024: D32 forward 1.43 -> 1.17 ms, D64 1.23 -> 1.19 ms).
   p->KS = (KT >= 4 || p->NDT == 1) ? 4 : (KT >= 2 ? 2 : 1);
-  // eight where each wave would otherwise poll four or more k-tiles (D >= 512:
-  // LSTM B16 T1024 D512 forward 2.31 -> 1.86 ms; at D256, B8, 1.25 -> 1.30)
-  if (p->NDT == 1 && KT >= 16 && fits(*p, 8, true)) p->KS = 8;
+  // eight from D384 (each wave would otherwise poll three or more k-tiles), and
+  // at D256 with more than 8 batch rows (measured, forward: LSTM B16 T1024
+  // D512 2.31 -> 1.86 ms, D384 1.83 -> 1.47 ms, B8 D384 1.64 -> 1.32 ms;
+  // B16 D256 GRU 0.66 -> 0.58, Elman 0.64 -> 0.53, LSTM 1.39 -> 1.37 ms;
+  // but at B <= 8 and D256 every cell was 2-10% slower)
+  if (p->NDT == 1 && (KT >= 12 || (KT >= 8 && p->B > 8)) && fits(*p, 8, true)) p->KS = 8;
   if (p->NDT == 1 && KT < 4 && !fits(*p, 4, true)) p->KS = KT >= 2 ? 2 : 1;
   if (p->NDT == 2 && !fits(*p, 4, true)) p->KS = 3;
   // (also where the backward's operand alone is wide: G_R*D/32 >= 16, LSTM

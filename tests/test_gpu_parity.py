@@ -80,6 +80,9 @@ CASES = [
     ("lstm", 16, 11, 2, 128),
     ("slstm", 4, 9, 2, 128),
     ("gru", 9, 8, 2, 96),
+    # 8 forward waves at D384, and at D256 with more than 8 batch rows
+    ("lstm", 6, 9, 1, 384),
+    ("elman", 12, 9, 2, 256),
 ]
 
 
