@@ -235,7 +235,7 @@ int make_plan(const frnn_desc* d, Plan* p) {
   auto ks_env = [&](const char* name, int* ks) {
     if (const char* e = std::getenv(name)) {
       const int v = std::atoi(e);
-      if ((v == 1 || v == 2 || v == 4 || (v == 8 && p->NDT == 1) || (v == 3 && p->NDT == 2)) && (v <= KT || v <= 4))
+      if ((v == 1 || v == 2 || v == 4 || (v == 8 && p->NDT == 1) || (v == 3 && p->NDT == 2)) && (v <= KT || v <= 4 || (v == 8 && KT >= 4)))
         *ks = v;
     }
   };
@@ -346,7 +346,9 @@ int groups_per_launch(const Plan& p, const void* fn, int block, size_t lds, int*
   if (p.flags & FRNN_XCD_SHARED)
     g = (long long)cus * per_cu / p.wpg;
   else
-    g = (long long)frnn::kXcds * ((long long)(cus / frnn::kXcds) * per_cu / (p.wpg + ((p.flags & frnn::kFlagScout) ? 1 : 0)));
+    g = (long long)frnn::kXcds *
+        ((long long)(cus / frnn::kXcds) * per_cu /
+         (p.wpg + ((p.flags & frnn::kFlagScout) ? std::max(1, p.nscout) : 0)));
   if (g < 1) return FRNN_E_UNSUPPORTED;
   *per_launch = (int)std::min<long long>(g, p.ngroups);
   return FRNN_OK;
@@ -359,20 +361,42 @@ int groups_per_launch(const Plan& p, const void* fn, int block, size_t lds, int*
 // scout's HBM loads would otherwise hold up the polls of a member on its CU
 // (and two members on one CU hold up each other's). Sets kFlagScout in the
 // launch plan *ap, the groups per launch and the dynamic LDS of the launch.
-void use_scouts(const Plan& p, const void* fn, int block, size_t* lds, Plan* ap, int* per_launch) {
+// Up to `nscout` scouts per group share its touches (fewer where more would
+// take another launch).
+void use_scouts(const Plan& p, const void* fn, int block, size_t* lds, Plan* ap, int* per_launch, int nscout = 1) {
   if ((p.flags & (FRNN_XCD_SHARED | FRNN_GRAD_CUT)) || g_no_scout.load()) return;
   constexpr size_t kHalfCu = 80 * 1024;
   const size_t lds1 = *lds > kHalfCu ? *lds : kHalfCu + 1024;
   if (set_lds_limit(fn, lds1) != FRNN_OK || blocks_per_cu(fn, block, lds1) != 1) return;
-  Plan ps = p;
-  ps.flags |= frnn::kFlagScout;
-  int per_scout = 0;
-  if (groups_per_launch(ps, fn, block, lds1, &per_scout) == FRNN_OK &&
-      (p.ngroups + per_scout - 1) / per_scout == (p.ngroups + *per_launch - 1) / *per_launch) {
-    ap->flags |= frnn::kFlagScout;
-    *per_launch = per_scout;
-    *lds = lds1;
+  for (int nsc = std::max(1, nscout); nsc >= 1; --nsc) {
+    Plan ps = p;
+    ps.flags |= frnn::kFlagScout;
+    ps.nscout = nsc;
+    int per_scout = 0;
+    if (groups_per_launch(ps, fn, block, lds1, &per_scout) == FRNN_OK &&
+        (p.ngroups + per_scout - 1) / per_scout == (p.ngroups + *per_launch - 1) / *per_launch) {
+      ap->flags |= frnn::kFlagScout;
+      ap->nscout = nsc;
+      *per_launch = per_scout;
+      *lds = lds1;
+      return;
+    }
   }
+}
+
+// Scouts per group in the backward: one per kScoutLines touch slots of a step
+// (a scout's CU keeps only so many lines in flight; one that falls behind its
+// pace touches lines the I/O waves have already missed on). FRNN_SCOUT_LINES
+// (environment, read per call) overrides the share.
+int bwd_scouts(const Plan& p) {
+  constexpr int kScoutLines = 512;
+  int cap = kScoutLines;
+  if (const char* e = std::getenv("FRNN_SCOUT_LINES"))
+    if (std::atoi(e) > 0) cap = std::atoi(e);
+  const int nst = (p.flags & FRNN_OUT_HIDDEN) ? 1 : p.S;
+  const int lines = frnn::bwd_scout_lines(p, nst, std::min(p.BS, p.B), p.dt_out == FRNN_F32 ? 4 : 2,
+                                          p.dt_save == FRNN_F32 ? 4 : 2);
+  return std::min(8, std::max(1, (lines + cap - 1) / cap));
 }
 
 // Launch the persistent kernel over all groups in as few launches as residency
@@ -684,7 +708,7 @@ int frnn_bwd(const frnn_desc* d, const void* R, const void* s0, const void* stat
   int per_launch = 0;
   if ((rc = set_lds_limit(fn, lds)) != FRNN_OK) return rc;
   if ((rc = groups_per_launch(p, fn, block, lds, &per_launch)) != FRNN_OK) return rc;
-  use_scouts(p, fn, block, &lds, &a.p, &per_launch);
+  use_scouts(p, fn, block, &lds, &a.p, &per_launch, bwd_scouts(p));
   hipEvent_t t0;
   bool timed = timing_begin(st, &t0);
   rc = launch_groups(&a.p, fn, block, lds, &a, per_launch, st);

@@ -65,6 +65,7 @@ struct Plan {
   int dma_gemm;                       // backward: the dR GEMM runs on the LDS-DMA kernel
   int rs;                             // backward: reduce-scatter exchange (bwd_rs_kernel)
   int ptm;                            // reduce-scatter: output tiles per compute wave (class)
+  int nscout;                         // scouts per group in a launch with kFlagScout (>= 1)
 };
 
 // Group / tile of a workgroup; returns false for an idle workgroup.
@@ -89,14 +90,16 @@ inline bool wg_decode(const Plan& p, int wg, int xcd, int* group, int* member) {
   return local < p.gcount;
 }
 
-// Scouts (kFlagScout, XCD-local exchange only) are the last 8 * ceil(gcount / 8)
-// workgroups of a launch's grid, after the members' slots; each claims, on its
-// own counters, the next group of the XCD it runs on.
+// Scouts (kFlagScout, XCD-local exchange only) are the last
+// 8 * ceil(gcount / 8) * nscout workgroups of a launch's grid, after the
+// members' slots; each claims, on its own counters, the next slot of the XCD
+// it runs on: slot / nscout is the group (of that XCD), slot % nscout the
+// scout's share of the group's touches.
 #if defined(__HIPCC__)
 __host__ __device__
 #endif
 inline int scout_blocks(const Plan& p) {
-  return (p.flags & kFlagScout) ? kXcds * ((p.gcount + kXcds - 1) / kXcds) : 0;
+  return (p.flags & kFlagScout) ? kXcds * ((p.gcount + kXcds - 1) / kXcds) * (p.nscout > 1 ? p.nscout : 1) : 0;
 }
 
 // ---------------------------------------------------------------- addressing
@@ -155,6 +158,14 @@ FRNN_HD inline long carry_index(const Plan& p, int k, int b, int n, int d) {
 FRNN_HD inline long save_index(const Plan& p, int ne, int t, int wgi, int v, int team, int e) {
   const long per = (long)p.NDT * ne;
   return (((long)t * p.nwg + wgi) * p.nsave + v) * per + (long)team * ne + e;
+}
+
+// Backward scout: touch slots of one step for a group (state-cotangent lines,
+// nst values of nreal rows at esz bytes; then every 128-byte line of the
+// group's saved values at ssz bytes), shared out among the group's scouts.
+FRNN_HD inline int bwd_scout_lines(const Plan& p, int nst, int nreal, int esz, int ssz) {
+  const int lpr = (p.D * esz + 127) / 128 + 1;  // lines of one row (+1: unaligned rows)
+  return nst * nreal * lpr + p.wpg * p.nsave * p.NDT * p.NB * 2 * ssz;
 }
 
 // Exchange word of (row r, contraction index k) in one group's table, chunk-major

@@ -153,9 +153,12 @@ __device__ __forceinline__ bool scout_setup(const Plan& p, Team& tm, uint32_t* c
   __syncthreads();
   const uint32_t slot = *s_slot;
   __syncthreads();
-  const int local = (int)slot * kXcds + xcd;
-  if (slot >= (uint32_t)((p.gcount + kXcds - 1) / kXcds) || local >= p.gcount) return false;
+  const int nsc = p.nscout > 1 ? p.nscout : 1;
+  if (slot >= (uint32_t)((p.gcount + kXcds - 1) / kXcds * nsc)) return false;
+  const int local = (int)(slot / nsc) * kXcds + xcd;
+  if (local >= p.gcount) return false;
   tm.group = p.g0 + local;
+  tm.member = (int)(slot % nsc);  // this scout's share of the group's touches
   tm.n = tm.group / p.nslab;
   tm.slab = tm.group % p.nslab;
   return true;
@@ -775,7 +778,8 @@ __device__ void fwd_scout(const FwdArgs& a, const Team& tm, float* lds) {
   const int nt = nreal * GW * lpr;
   auto lptr = (__attribute__((address_space(3))) void*)(lds + (threadIdx.x >> 6) * 64);
   auto touch = [&](int u) {
-    for (int i = threadIdx.x; i < nt; i += blockDim.x) {
+    const int nsc = p.nscout > 1 ? p.nscout : 1;
+    for (int i = tm.member * blockDim.x + threadIdx.x; i < nt; i += nsc * blockDim.x) {
       const int r = i / (GW * lpr), g = (i / lpr) % GW, l = i % lpr;
       __builtin_amdgcn_global_load_lds(static_cast<const char*>(a.wx) + scout_wx_byte(p, tm.slab, tm.n, r, u, g, l, esz),
                                        lptr, 4, 0, 0);
@@ -1215,11 +1219,12 @@ __device__ void bwd_scout(const BwdArgs& a, const Team& tm, float* lds) {
   const int nd = nst * nreal * lpr;                                    // state-cotangent touches
   const int ssz = p.dt_save == DT_F32 ? 4 : 2;                         // bytes of a saved value
   const int lpt = 2 * ssz;                                             // lines of a 16-row tile of one value
-  const int ns = p.wpg * p.nsave * p.NDT * p.NB * lpt;                 // save touches
+  const int nall = bwd_scout_lines(p, nst, nreal, esz, ssz);           // nd + the save touches
+  const int nsc = p.nscout > 1 ? p.nscout : 1;
   auto lptr = (__attribute__((address_space(3))) void*)(lds + (threadIdx.x >> 6) * 64);
   auto touch = [&](int it) {
     const int t = T - 1 - it;
-    for (int i = threadIdx.x; i < nd + ns; i += blockDim.x) {
+    for (int i = tm.member * blockDim.x + threadIdx.x; i < nall; i += nsc * blockDim.x) {
       const char* src = nullptr;
       if (i < nd) {
         const int k = i / (nreal * lpr), r = (i / lpr) % nreal, l = i % lpr;
