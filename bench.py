@@ -287,6 +287,9 @@ def main(argv=None):
     ap.add_argument("--projection-only", action="store_true",
                     help="only the forward of the layer-with-input-projection side measurement (one JSON line, "
                          "not the metric; the command its rocprof summaries were made with)")
+    ap.add_argument("--configs-only", action="store_true",
+                    help="only the other configurations' fwd+bwd timings (one JSON line, not the metric; the "
+                         "command their rocprof summary was made with)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a plain device copy of MIB MiB (5 times): the reference point that scales "
                          "the FETCH_SIZE / WRITE_SIZE counters to bytes")
@@ -315,6 +318,10 @@ def main(argv=None):
     from flashrnn_amd import _lib, flashrnn, synchronize_and_check
 
     dev = torch.device("cuda", 0)
+    if args.configs_only:
+        print(json.dumps({"other_configs": other_configs(torch, dev, flashrnn)}), flush=True)
+        synchronize_and_check()
+        return 0
     if args.projection_only:
         print(json.dumps({"input_projection": projection_layer(torch, dev, with_backward=False)}), flush=True)
         synchronize_and_check()
