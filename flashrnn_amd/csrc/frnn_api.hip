@@ -85,7 +85,7 @@ int nsave_of(int cell) {
     case FRNN_LSTM: return 6;
     case FRNN_GRU: return 5;
     case FRNN_ELMAN: return 1;
-    case FRNN_SLSTM: return 11;
+    case FRNN_SLSTM: return 8;
   }
   return 0;
 }
@@ -690,6 +690,7 @@ int frnn_bwd(const frnn_desc* d, const void* R, const void* s0, const void* stat
   a.p = p;
   a.R = R;
   a.save = save;
+  a.s0 = s0;
   a.d_states = d_states;
   a.d_carry = d_carry;
   a.dwx = dwx;

@@ -178,6 +178,15 @@ __global__ void __launch_bounds__(64 * (KSC + 1) * NDT) bwd_rs_kernel(BwdArgs a)
 #pragma unroll
     for (int g = 0; g < GT; ++g) dbacc[s][g] = 0.f;
   }
+  // sLSTM: (c, n) of the initial state, the (c_{t-1}, n_{t-1}) of step 0
+  float init_cn[EPLMAX][2];
+#pragma unroll
+  for (int s = 0; s < EPLMAX; ++s)
+#pragma unroll
+    for (int k = 0; k < 2; ++k)
+      init_cn[s][k] = (CELL == CELL_SLSTM && el[s].real)
+                          ? ld_val(a.s0, carry_index(p, 1 + k, el[s].b, tm.n, el[s].d), p.dt_state)
+                          : 0.f;
   // B operand lanes: column c = lane % 16 is batch row c, or with at most 8 real
   // rows (paired) row c % 8, the hi part in columns 0-7 and the lo part in 8-15
   const bool pair = B <= 8;
@@ -222,8 +231,16 @@ __global__ void __launch_bounds__(64 * (KSC + 1) * NDT) bwd_rs_kernel(BwdArgs a)
       float sv[NSAVE];
 #pragma unroll
       for (int v = 0; v < NSAVE; ++v) sv[v] = in[S + v];
+      // sLSTM: c and n of step t-1 from that step's saves (staged for the next
+      // iteration before the previous barrier), or the initial state at t = 0
+      float prev[2] = {0.f, 0.f};
+      if constexpr (CELL == CELL_SLSTM) {
+        const float* irn = iring + (long)((it + 1) % kBwdStage) * NIN * NE;
+#pragma unroll
+        for (int k = 0; k < 2; ++k) prev[k] = it + 1 < T ? irn[(S + 1 + k) * NE + e] : init_cn[s][k];
+      }
       float dry[GR], dwx[GW], db[GT], cr[S];
-      Cell<CELL>::bwd(ds, sv, dry, dwx, db, cr, v1);
+      Cell<CELL>::bwd(ds, sv, prev, dry, dwx, db, cr, v1);
       if (!el[s].real) {
 #pragma unroll
         for (int g = 0; g < GR; ++g) dry[g] = 0.f;

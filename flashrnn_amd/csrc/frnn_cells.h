@@ -9,9 +9,14 @@
 //   LSTM  : sig(i) sig(f) tanh(z) sig(o) tanh(c_t) c_{t-1}
 //   GRU   : r u v cand h_{t-1}
 //   Elman : h_t
-//   sLSTM : sig(o) c_t n_t tanh(z) i' f' c_{t-1} n_{t-1} sig(-f) w_n w_m
+//   sLSTM : sig(o) c_t n_t tanh(z) i' f' sig(-f) 8 w_m + 2 w_n
 //           (w_n: share of the cotangent of max(npre, 1) that reaches npre;
-//            w_m: share of the cotangent of m that reaches the input gate)
+//            w_m: share of the cotangent of m that reaches the input gate; each
+//            is 0, 1/2 or 1, so the integer code holds both exactly). c_{t-1} and
+//            n_{t-1} are not saved: they are c and n of step t-1 (the initial
+//            state at t = 0), which the backward reads from that step's saves.
+//
+// Backward: prev holds (c_{t-1}, n_{t-1}) for the sLSTM; the other cells ignore it.
 #pragma once
 
 #include "frnn_device.h"
@@ -34,7 +39,7 @@ template <> struct Cell<CELL_LSTM> {
   }
   // ds: total cotangents of (h_t, c_t). Out: dry (= dWx), cotangent carried to
   // (h_{t-1}, c_{t-1}) through direct (non-recurrent) paths.
-  __device__ __forceinline__ static void bwd(const float* ds, const float* sv, float* dry, float* dwx,
+  __device__ __forceinline__ static void bwd(const float* ds, const float* sv, const float*, float* dry, float* dwx,
                                              float* db, float* carry, bool v1) {
     const float si = sv[0], sf = sv[1], tz = sv[2], so = sv[3], tc = sv[4], cp = sv[5];
     const float dh = ds[0];
@@ -64,7 +69,7 @@ template <> struct Cell<CELL_GRU> {
     sv[0] = r; sv[1] = u; sv[2] = v; sv[3] = cand; sv[4] = st[0];
     st[0] = u * st[0] + (1.f - u) * v;
   }
-  __device__ __forceinline__ static void bwd(const float* ds, const float* sv, float* dry, float* dwx,
+  __device__ __forceinline__ static void bwd(const float* ds, const float* sv, const float*, float* dry, float* dwx,
                                              float* db, float* carry, bool v1) {
     const float r = sv[0], u = sv[1], v = sv[2], cand = sv[3], hp = sv[4];
     const float dh = ds[0];
@@ -86,7 +91,7 @@ template <> struct Cell<CELL_ELMAN> {
     st[0] = tanhf_(g[0]);
     sv[0] = st[0];
   }
-  __device__ __forceinline__ static void bwd(const float* ds, const float* sv, float* dry, float* dwx,
+  __device__ __forceinline__ static void bwd(const float* ds, const float* sv, const float*, float* dry, float* dwx,
                                              float* db, float* carry, bool v1) {
     const float h = sv[0];
     const float da = ds[0] * (1.f - h * h);
@@ -97,7 +102,7 @@ template <> struct Cell<CELL_ELMAN> {
 
 // ------------------------------------------------------------------ sLSTM
 template <> struct Cell<CELL_SLSTM> {
-  static constexpr int NSAVE = 11;
+  static constexpr int NSAVE = 8;
   // st: (h, c, n, m). zero: the global all-normalizers-zero predicate of this step.
   __device__ __forceinline__ static void fwd(const float* g, float* st, float* sv, uint32_t zero) {
     const float gi = g[0], gf = g[1], gz = g[2], go = g[3];
@@ -115,16 +120,18 @@ template <> struct Cell<CELL_SLSTM> {
     const float nn = fmaxf(npre, 1.f);
     const float wn = npre > 1.f ? 1.f : (npre == 1.f ? 0.5f : 0.f);
     sv[0] = so; sv[1] = c; sv[2] = nn; sv[3] = tz; sv[4] = ia; sv[5] = fa;
-    sv[6] = st[1]; sv[7] = st[2]; sv[8] = sigmoidf_(-gf); sv[9] = wn; sv[10] = wm;
+    sv[6] = sigmoidf_(-gf); sv[7] = 8.f * wm + 2.f * wn;
     st[0] = so * c / nn;
     st[1] = c;
     st[2] = nn;
     st[3] = m;
   }
-  __device__ __forceinline__ static void bwd(const float* ds, const float* sv, float* dry, float* dwx,
-                                             float* db, float* carry, bool v1) {
+  __device__ __forceinline__ static void bwd(const float* ds, const float* sv, const float* prev, float* dry,
+                                             float* dwx, float* db, float* carry, bool v1) {
     const float so = sv[0], c = sv[1], nn = sv[2], tz = sv[3], ia = sv[4], fa = sv[5];
-    const float cold = sv[6], nold = sv[7], sgn = sv[8], wn = sv[9], wm = sv[10];
+    const float cold = prev[0], nold = prev[1], sgn = sv[6];
+    const float wq = floorf(0.25f * sv[7]);  // 2 w_m (sv[7] = 4 (2 w_m) + 2 w_n, an integer)
+    const float wm = 0.5f * wq, wn = 0.5f * (sv[7] - 4.f * wq);
     const float dh = ds[0];
     const float rn = 1.f / nn;
     const float dgo = dh * c * rn * so * (1.f - so);

@@ -67,6 +67,7 @@ struct BwdArgs {
   Plan p;
   const void* R;
   const void* save;         // lane-native saved values (dtype p.dt_save)
+  const void* s0;           // initial states [S][B][N][D] (dtype p.dt_state): the sLSTM's c_{-1}, n_{-1}
   const void* d_states;     // may be null
   const void* d_carry;      // may be null
   void* dwx;

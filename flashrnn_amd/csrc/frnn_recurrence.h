@@ -1390,6 +1390,15 @@ __global__ void __launch_bounds__(64 * (KSC + 1) * NDT) bwd_kernel(BwdArgs a) {
 #pragma unroll
     for (int g = 0; g < GT; ++g) dbacc[s][g] = 0.f;
   }
+  // sLSTM: (c, n) of the initial state, the (c_{t-1}, n_{t-1}) of step 0
+  float init_cn[EPLMAX][2];
+#pragma unroll
+  for (int s = 0; s < EPLMAX; ++s)
+#pragma unroll
+    for (int k = 0; k < 2; ++k)
+      init_cn[s][k] = (CELL == CELL_SLSTM && el[s].real)
+                          ? ld_val(a.s0, carry_index(p, 1 + k, el[s].b, tm.n, el[s].d), p.dt_state)
+                          : 0.f;
 
   Prof prof;
   prof.init(a.prof != nullptr && blockIdx.x == 0, a.prof != nullptr);
@@ -1420,6 +1429,22 @@ __global__ void __launch_bounds__(64 * (KSC + 1) * NDT) bwd_kernel(BwdArgs a) {
       for (int k = 0; k < NIN; ++k) dst[s][k] = own[s] ? ir[k * NE + oe[s]] : 0.f;
   };
   read_in(0, in_cur);
+  // sLSTM: (c_{t-1}, n_{t-1}) of iteration j are c and n of step t-1, saved in
+  // the inputs of iteration j+1 (the initial state at the last iteration); they
+  // are read during the previous iteration's reduction, once the barrier has
+  // made that ring slot complete
+  float prev_cn[EPLMAX][2];
+  auto read_prev = [&](int j) {
+#pragma unroll
+    for (int s = 0; s < EPLMAX; ++s) {
+      const float* irn = iring + (long)((j + 1) % kBwdStage) * NIN * NE;
+#pragma unroll
+      for (int k = 0; k < 2; ++k)
+        prev_cn[s][k] = CELL != CELL_SLSTM ? 0.f : (j + 1 < T ? (own[s] ? irn[(S + 1 + k) * NE + oe[s]] : 0.f)
+                                                              : init_cn[s][k]);
+    }
+  };
+  read_prev(0);
   bool abort = false;
   for (int it = 0; it < T; ++it) {
     prof.stamp(it, 0);
@@ -1449,7 +1474,7 @@ __global__ void __launch_bounds__(64 * (KSC + 1) * NDT) bwd_kernel(BwdArgs a) {
 #pragma unroll
       for (int v = 0; v < NSAVE; ++v) sv[v] = in[S + v];
       float dry[GR], dwx[GW], db[GT], cr[S];
-      Cell<CELL>::bwd(ds, sv, dry, dwx, db, cr, v1);
+      Cell<CELL>::bwd(ds, sv, prev_cn[s], dry, dwx, db, cr, v1);
       if (!el[s].real) {
 #pragma unroll
         for (int g = 0; g < GR; ++g) dry[g] = 0.f;
@@ -1544,6 +1569,8 @@ __global__ void __launch_bounds__(64 * (KSC + 1) * NDT) bwd_kernel(BwdArgs a) {
     prof.stamp(it, 3);
 
     // ---- 3. owners: reduce -> recurrent cotangent of h_{t-1}
+    if constexpr (CELL == CELL_SLSTM)
+      if (it + 1 < T) read_prev(it + 1);  // its ring slot was staged before this barrier
 #pragma unroll
     for (int s = 0; s < EPLMAX; ++s) {
       if (!own[s]) continue;
