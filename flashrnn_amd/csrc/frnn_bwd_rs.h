@@ -30,14 +30,14 @@
 namespace frnn {
 
 // Shape of the local contraction: k = o_local * GRP + g over the OL units of a
-// workgroup (GRP = 4 slots per unit for the gated cells, 1 for Elman; slots
-// with g >= GR are zero), padded to 32-wide k-tiles; LDS rows of the dG
-// operand are padded by 4 floats so the operand reads are conflict-free.
+// workgroup (GRP = GR slots per unit: 4 for the LSTM and sLSTM, 3 for the GRU,
+// 1 for Elman), padded to 32-wide k-tiles; LDS rows of the dG operand are
+// padded by 4 floats so the operand reads are conflict-free.
 template <int CELL, int NDT>
 struct RsShape {
   static constexpr int GR = CellShape<CELL>::GR;
   static constexpr int OL = 16 * NDT;
-  static constexpr int GRP = GR == 1 ? 1 : 4;
+  static constexpr int GRP = GR;
   static constexpr int KTL = (OL * GRP + 31) / 32;
   static constexpr int KROW = KTL * 32 + 4;
   // floats of LDS: the dG operand [2][16][KROW], then per team the input ring
@@ -262,7 +262,8 @@ __global__ void __launch_bounds__(64 * (KSC + 1) * NDT) bwd_rs_kernel(BwdArgs a)
         for (int g = 0; g < GR; ++g) v4[g] = dry[g];
         *reinterpret_cast<f32x4*>(drow) = v4;
       } else {
-        drow[0] = dry[0];
+#pragma unroll
+        for (int g = 0; g < GRP; ++g) drow[g] = dry[g];
       }
 #pragma unroll
       for (int g = 0; g < GW; ++g) os[g * NE + e] = dwx[g];
