@@ -974,6 +974,10 @@ __global__ void __launch_bounds__(64 * (KSC + 1) * NDT) fwd_kernel(FwdArgs a) {
   // from the ring while step t's first poll is in flight (gather's `between`):
   // the poll goes out right after the loop head. The staging area of step t-1
   // is drained after barrier t, its ring slot was filled before barrier t-1.
+  // Two-tile workgroups stage each step's outputs right after its cell instead
+  // (slot t & 1, which the I/O wave drains after barrier t + 1): the saved
+  // values then need no registers across the poll, where these kernels run out
+  constexpr bool kStageNow = NDT == 2;
   float sv_keep[EPLMAX][NSAVE];
   auto stage = [&](int t) {
     float* os = ost + (long)(t & 1) * NV * NE;
@@ -1003,7 +1007,7 @@ __global__ void __launch_bounds__(64 * (KSC + 1) * NDT) fwd_kernel(FwdArgs a) {
       for (int g = 0; g < GR; ++g) acc[bt][g] = mma(A[g][j], f, acc[bt][g]);
     };
     auto between = [&]() {
-      if (t >= 1) stage(t - 1);
+      if (!kStageNow && t >= 1) stage(t - 1);
       read_x(t);
     };
     {
@@ -1075,11 +1079,18 @@ __global__ void __launch_bounds__(64 * (KSC + 1) * NDT) fwd_kernel(FwdArgs a) {
       if (s == 0) prof.stamp(t, 3);
 #pragma unroll
       for (int v = 0; v < NSAVE; ++v) sv_keep[s][v] = sv[v];
+      if constexpr (kStageNow) {
+        float* os = ost + (long)(t & 1) * NV * NE;
+#pragma unroll
+        for (int k = 0; k < S; ++k) os[k * NE + e] = st[s][k];
+#pragma unroll
+        for (int v = 0; v < NSAVE; ++v) os[(S + v) * NE + e] = sv[v];
+      }
     }
     prof.mark(3);
     prof.stamp(t, 4);
   }
-  stage(T - 1);
+  if (!kStageNow) stage(T - 1);
   lds_barrier();  // the I/O wave drains the last step
 
   // ---- carry: the last state in full precision
