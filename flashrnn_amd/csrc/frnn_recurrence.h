@@ -975,8 +975,9 @@ __global__ void __launch_bounds__(64 * (KSC + 1) * NDT) fwd_kernel(FwdArgs a) {
   // the poll goes out right after the loop head. The staging area of step t-1
   // is drained after barrier t, its ring slot was filled before barrier t-1.
   // Two-tile workgroups stage each step's outputs right after its cell instead
-  // (slot t & 1, which the I/O wave drains after barrier t + 1): the saved
-  // values then need no registers across the poll, where these kernels run out
+  // (slot t & 1, which the I/O wave drains after barrier t + 1) and read the
+  // step's Wx with the partial sums: neither needs registers across the poll,
+  // where these kernels run out
   constexpr bool kStageNow = NDT == 2;
   float sv_keep[EPLMAX][NSAVE];
   auto stage = [&](int t) {
@@ -1008,7 +1009,7 @@ __global__ void __launch_bounds__(64 * (KSC + 1) * NDT) fwd_kernel(FwdArgs a) {
     };
     auto between = [&]() {
       if (!kStageNow && t >= 1) stage(t - 1);
-      read_x(t);
+      if (!kStageNow) read_x(t);
     };
     {
       uint32_t polls;
@@ -1051,8 +1052,14 @@ __global__ void __launch_bounds__(64 * (KSC + 1) * NDT) fwd_kernel(FwdArgs a) {
 #pragma unroll
       for (int w2 = 0; w2 < KS; ++w2) part[w2] = *reinterpret_cast<const f32x4*>(rp + w2 * NB * RED_F + src);
       float xcur[GW];
+      if constexpr (kStageNow) {  // read with the partial sums (slot t % kFwdXf is kept until barrier t + 1)
+        const float* xr = xf + (long)(t % kFwdXf) * Lds<CELL, NB>::XF;
 #pragma unroll
-      for (int g = 0; g < GW; ++g) xcur[g] = xnext[s][g];
+        for (int g = 0; g < GW; ++g) xcur[g] = xr[g * NE + e];
+      } else {
+#pragma unroll
+        for (int g = 0; g < GW; ++g) xcur[g] = xnext[s][g];
+      }
       float ry[GR];
 #pragma unroll
       for (int g = 0; g < GR; ++g) {
