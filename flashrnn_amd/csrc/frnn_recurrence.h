@@ -1436,8 +1436,12 @@ __global__ void __launch_bounds__(64 * (KSC + 1) * NDT) bwd_kernel(BwdArgs a) {
   // during this iteration's poll (the I/O wave staged them before the previous
   // barrier), so no LDS read stands between the loop head and the pointwise
   // backward. Two-tile workgroups (two elements per lane, 256 registers a wave)
-  // have no registers for a second set and read them at the loop head.
-  constexpr bool kPrefetch = NDT == 1;
+  // have no registers for a second set and read them at the loop head, and so
+  // does the LSTM with two or more k-tiles per wave in eight waves (168
+  // registers a wave): the second set made it spill, B16 T1024 backward D512
+  // 4.19 -> 3.83 ms and N2 D384 3.45 -> 2.98 ms without it (the GRU and sLSTM
+  // there were 5-9% slower without it).
+  constexpr bool kPrefetch = NDT == 1 && !(CELL == CELL_LSTM && KS == 8 && KTW >= 2);
   float in_cur[EPLMAX][NIN], in_next[kPrefetch ? EPLMAX : 1][NIN];
   auto read_in = [&](int it, auto& dst) {
     const float* ir = iring + (long)(it % kBwdStage) * NIN * NE;
