@@ -927,6 +927,7 @@ __global__ void __launch_bounds__(64 * (KSC + 1) * NDT) fwd_kernel(FwdArgs a) {
 #pragma unroll
   for (int j = 0; j < KTW; ++j) xword_pair[j] = xgrp + xword_of<MMA>(p.BS, tm.lane & 7, (kt0 + j) * 32 + 8 * tm.kq);
   const bool bv_pair = (tm.lane & 7) < B;
+  const int xkstride = xword_of<MMA>(p.BS, 0, 32) - xword_of<MMA>(p.BS, 0, 0);  // words between k-tiles
 
   // ---- owned elements
   int oe[EPLMAX];
@@ -1014,10 +1015,22 @@ __global__ void __launch_bounds__(64 * (KSC + 1) * NDT) fwd_kernel(FwdArgs a) {
     {
       uint32_t polls;
       const int off = ((t - 1) & 1) * xpar;
-      if (NB == 1 && pair)
-        polls = gather_pair_mma<MMA, NDT, KTW>(xc, xword_pair, bv_pair, off, cstride, nkt, ptag(p, t - 1), a.status,
+      if (NB == 1 && pair) {
+        // two-tile workgroups: the paired runs' words rebuilt each step from one
+        // base (they are linear in the k-tile), so they hold no registers across
+        // the loop where the unpaired runs are polled
+        int xwp[KTW];
+#pragma unroll
+        for (int j = 0; j < KTW; ++j) xwp[j] = xword_pair[j];
+        if constexpr (NDT == 2) {
+          int bp = xword_pair[0];
+          asm volatile("" : "+v"(bp));
+#pragma unroll
+          for (int j = 0; j < KTW; ++j) xwp[j] = bp + j * xkstride;
+        }
+        polls = gather_pair_mma<MMA, NDT, KTW>(xc, xwp, bv_pair, off, cstride, nkt, ptag(p, t - 1), a.status,
                                                a.spin_limit, abort, zero, prod, between);
-      else
+      } else
         // pipelined chunks where the unpacked chunk fits beside the resident R
         // (GR * KTW <= 24: measured at D768 GRU 1.62 -> 1.58 ms; the LSTM's 32
         // spilled, 4.19 -> 4.92 ms)
