@@ -232,6 +232,15 @@ int make_plan(const frnn_desc* d, Plan* p) {
   p->KSB = ((KT >= 8 || p->kt_bwd >= 16) && p->NDT == 1) ? 8 : p->KS;
   if (p->NDT == 1 && p->KSB == 8 && !fits(*p, 8, false)) p->KSB = 4;
   if (p->NDT == 2 && !fits(*p, p->KSB, false)) p->KSB = 3;
+  // two-tile workgroups whose reduce-scatter backward is built with four compute
+  // waves per tile (the GRU; up to 48 tiles: six output tiles a wave) take it:
+  // every SIMD then runs two of the eight compute waves' MFMAs (GRU B16 T512
+  // D768 backward 3.10 -> 2.48 ms, D640 3.00 -> 2.33 ms; the LSTM's spilled)
+  {
+    const char* e = std::getenv("FRNN_BWD_RS");
+    if (p->NDT == 2 && p->D / 16 <= 48 && !(e && *e == '0') && frnn::rs_kernel(p->cell, p->mma, 2, 4, 6))
+      p->KSB = 4;
+  }
   auto ks_env = [&](const char* name, int* ks) {
     if (const char* e = std::getenv(name)) {
       const int v = std::atoi(e);
@@ -241,7 +250,7 @@ int make_plan(const frnn_desc* d, Plan* p) {
   };
   ks_env("FRNN_KS", &p->KS);
   ks_env("FRNN_KS_BWD", &p->KSB);
-  if (!fits(*p, p->KS, true) || !fits(*p, p->KSB, false)) return FRNN_E_UNSUPPORTED;
+  if (!fits(*p, p->KS, true)) return FRNN_E_UNSUPPORTED;
   p->epl = (4 * p->NB + p->KS - 1) / p->KS;
   p->nsave = nsave_of(p->cell);
   p->wpg = p->D / (16 * p->NDT);
@@ -259,13 +268,16 @@ int make_plan(const frnn_desc* d, Plan* p) {
   {
     const int ntile = p->D / 16, ncw = p->NDT * p->KSB;
     const int need = (ntile + ncw - 1) / ncw;
-    p->ptm = need <= 2 ? 2 : (need <= 4 ? 4 : (need <= 8 ? 8 : (need <= 16 ? 16 : 0)));
+    p->ptm = 0;  // the smallest built class that covers the need
+    for (int c : {2, 4, 6, 8, 16})
+      if (!p->ptm && need <= c && frnn::rs_kernel(p->cell, p->mma, p->NDT, p->KSB, c)) p->ptm = c;
     const char* e = std::getenv("FRNN_BWD_RS");
     const bool off = e && *e == '0';
-    p->rs = (!off && p->NDT == 2 && p->ptm && p->wpg <= 32 &&
+    p->rs = (!off && p->NDT == 2 && p->ptm && p->wpg <= p->ptm * p->KSB &&
              frnn::rs_kernel(p->cell, p->mma, p->NDT, p->KSB, p->ptm) != nullptr) ? 1 : 0;
     if (p->rs) p->xwords_bwd = (long long)p->ngroups * p->D * 16 * p->wpg;
   }
+  if (!p->rs && !fits(*p, p->KSB, false)) return FRNN_E_UNSUPPORTED;
   p->save_floats = (long long)p->T * p->nwg * p->nsave * p->NDT * 256 * p->NB;
   // dR GEMM: 64x64 workgroup tiles where D % 64 == 0 (else 32x32), split over
   // K = B*T to fill the GPU (~2048 workgroups, >= 8 k-steps of 32 each): the

@@ -59,6 +59,9 @@ static const void* pick_rs() {
 template <int MMA>
 static const void* rs_by_shape(int ndt, int ks, int ptm) {
   if (ndt == 2 && ks == 3 && ptm == 8) return pick_rs<MMA, 2, 3, 8>();
+  // four compute waves per tile (ten waves: two compute waves on every SIMD
+  // instead of three SIMDs with two and one with the two I/O waves)
+  if (ndt == 2 && ks == 4 && ptm == 6) return pick_rs<MMA, 2, 4, 6>();
   return nullptr;
 }
 

@@ -83,6 +83,8 @@ CASES = [
     # 8 forward waves at D384, and at D256 with more than 8 batch rows
     ("lstm", 6, 9, 1, 384),
     ("elman", 12, 9, 2, 256),
+    # the GRU's reduce-scatter backward with four compute waves per tile, paired polls
+    ("gru", 6, 9, 1, 640),
 ]
 
 
