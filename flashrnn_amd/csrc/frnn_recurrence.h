@@ -167,6 +167,18 @@ __device__ __forceinline__ bool scout_setup(const Plan& p, Team& tm, uint32_t* c
 // Element e of the team -> hidden unit d, slab row bl, batch row b.
 typedef ElemPos Elem;
 __device__ __forceinline__ Elem elem_of(const Plan& p, const Team& tm, int e) { return elem_pos(p, tm.slab, tm.dt, e); }
+// Owner slot i (s * KS * 64 + compute wave * 64 + lane) -> element in the
+// one-tile forward: the 16 rows of a batch tile are dealt to the slots'
+// 16-lane quarters round-robin (quarter q takes row 4 (q % 4) + q / 4: the
+// owner waves of four compute waves hold rows kw, kw + 4, kw + 8, kw + 12), so
+// a slab with fewer than 16 real rows still gives every owner wave a share of
+// the real work (measured, LSTM T1024 N3 D256 forward: B8 1.28 -> 1.25 ms, B4
+// 1.30 -> 1.24, B16 1.41 -> 1.38; the backward and the two-tile forward were
+// slower with it and keep slot order).
+__device__ __forceinline__ int owner_elem(int i) {
+  const int q = (i >> 4) & 15;
+  return (i & ~255) | ((((q & 3) << 2) | (q >> 2)) << 4) | (i & 15);
+}
 // Position of element e in the MFMA output layout of its batch tile: lane
 // (dd/4)*16 + row, register dd%4 (dd = hidden unit in the tile), as lane*4 + reg.
 __device__ __forceinline__ int mfma_pos(int e) {
@@ -936,8 +948,8 @@ __global__ void __launch_bounds__(64 * (KSC + 1) * NDT) fwd_kernel(FwdArgs a) {
   float st[EPLMAX][S], bias[EPLMAX][GT];
 #pragma unroll
   for (int s = 0; s < EPLMAX; ++s) {
-    oe[s] = s * KS * 64 + tm.kw * 64 + tm.lane;
-    own[s] = oe[s] < NE;
+    own[s] = s * KS * 64 + tm.kw * 64 + tm.lane < NE;
+    oe[s] = NDT == 1 ? owner_elem(s * KS * 64 + tm.kw * 64 + tm.lane) : s * KS * 64 + tm.kw * 64 + tm.lane;
     el[s] = elem_of(p, tm, oe[s] & (NE - 1));
     el[s].real = el[s].real && own[s];
 #pragma unroll
