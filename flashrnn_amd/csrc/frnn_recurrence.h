@@ -173,8 +173,9 @@ __device__ __forceinline__ Elem elem_of(const Plan& p, const Team& tm, int e) { 
 // owner waves of four compute waves hold rows kw, kw + 4, kw + 8, kw + 12), so
 // a slab with fewer than 16 real rows still gives every owner wave a share of
 // the real work (measured, LSTM T1024 N3 D256 forward: B8 1.28 -> 1.25 ms, B4
-// 1.30 -> 1.24, B16 1.41 -> 1.38; the backward and the two-tile forward were
-// slower with it and keep slot order).
+// 1.30 -> 1.24, B16 1.41 -> 1.38; the backward, the two-tile forward and the
+// sLSTM forward (C4 B16 D192 2.81 -> 2.93 ms: more staged values, whose LDS
+// writes the round-robin rows spread over fewer banks) keep slot order).
 __device__ __forceinline__ int owner_elem(int i) {
   const int q = (i >> 4) & 15;
   return (i & ~255) | ((((q & 3) << 2) | (q >> 2)) << 4) | (i & 15);
@@ -949,7 +950,8 @@ __global__ void __launch_bounds__(64 * (KSC + 1) * NDT) fwd_kernel(FwdArgs a) {
 #pragma unroll
   for (int s = 0; s < EPLMAX; ++s) {
     own[s] = s * KS * 64 + tm.kw * 64 + tm.lane < NE;
-    oe[s] = NDT == 1 ? owner_elem(s * KS * 64 + tm.kw * 64 + tm.lane) : s * KS * 64 + tm.kw * 64 + tm.lane;
+    oe[s] = (NDT == 1 && CELL != CELL_SLSTM) ? owner_elem(s * KS * 64 + tm.kw * 64 + tm.lane)
+                                             : s * KS * 64 + tm.kw * 64 + tm.lane;
     el[s] = elem_of(p, tm, oe[s] & (NE - 1));
     el[s].real = el[s].real && own[s];
 #pragma unroll
