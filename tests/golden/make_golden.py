@@ -49,8 +49,14 @@ def make_inputs(cell, B, T, N, D, dtype, seed, normalizer="nonzero"):
     return tensors, d_hist, d_last
 
 
-def run_case(flashrnn_torch, name, cell, numerics, dtype, normalizer="nonzero", B=3, T=6, N=2, D=8, seed=0):
+def run_case(flashrnn_torch, name, cell, numerics, dtype, normalizer="nonzero", B=3, T=6, N=2, D=8, seed=0,
+             bf16_exact=False):
     tensors, d_hist, d_last = make_inputs(cell, B, T, N, D, dtype, seed, normalizer)
+    if bf16_exact:
+        # every input and cotangent representable in BF16, so a BF16-tensor
+        # kernel can be checked against the reference's outputs directly
+        tensors = [t.bfloat16().to(dtype) for t in tensors]
+        d_hist, d_last = d_hist.bfloat16().to(dtype), d_last.bfloat16().to(dtype)
     leaves = [t.clone().requires_grad_() for t in tensors]
     hist, last = flashrnn_torch(*leaves, cell=cell, numerics=numerics)
     grads = torch.autograd.grad((hist * d_hist).sum() + (last * d_last).sum(), leaves)
@@ -78,6 +84,12 @@ def main():
                  normalizer=norm, seed=seed + 10 + k)
     run_case(flashrnn_torch, "bf16mma_slstm_zero", "slstm", "fp32_state_bf16_mma", torch.float32,
              normalizer="zero", seed=seed + 20)
+    # wider heads: several 32-wide MFMA k-tiles, padded widths, batch rows
+    # that do not fill a 16-row tile, more than one head
+    for k, (cell, B, T, N, D) in enumerate((("lstm", 10, 12, 2, 96), ("gru", 5, 10, 1, 64),
+                                            ("elman", 3, 9, 3, 48), ("slstm", 6, 10, 2, 64))):
+        run_case(flashrnn_torch, f"bf16mma_{cell}_wide", cell, "fp32_state_bf16_mma", torch.float32,
+                 B=B, T=T, N=N, D=D, seed=seed + 30 + k, bf16_exact=True)
 
 
 if __name__ == "__main__":

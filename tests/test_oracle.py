@@ -67,18 +67,26 @@ def test_golden_vectors_explicit_backward(path):
     bf = numerics == "fp32_state_bf16_mma"
     args = [z[k] for k in ("wx", "R", "b", "s0")]
     hist, _ = ne.forward(*args, cell, bf)
-    tol = 2e-5 if bf else 1e-12
-    assert np.abs(hist - z["hist"]).max() <= tol
+    # The NumPy restatement sums in its own order. In the BF16 policy a sum that
+    # lands next to a BF16 rounding boundary can round the other way, and the
+    # flip (2^-8 relative on one operand) carries through later steps. The
+    # wide cases (64-96 wide heads, 9-12 steps) have more such flips than the
+    # D=8 ones, so their bound is looser. The torch restatement above matches
+    # every case bit for bit.
+    wide = bf and z["wx"].shape[-1] > 8
+    tol = 1e-3 if wide else (2e-5 if bf else 1e-12)
+    assert np.abs(hist - z["hist"]).max() / np.abs(z["hist"]).max() <= tol
     grads = ne.backward(*args, cell, z["d_hist"], z["d_last"], bf)
     for g, k in zip(grads, ("dwx", "dR", "db", "ds0")):
         e = z[k]
-        assert np.abs(g - e).max() / np.abs(e).max() <= (1e-4 if bf else 1e-12), k
+        assert np.abs(g - e).max() / np.abs(e).max() <= (5e-3 if wide else 1e-4 if bf else 1e-12), k
 
 
 def test_golden_coverage():
     names = {os.path.basename(p)[:-4] for p in GOLDEN}
     assert {f"bf16mma_{c}" for c in SIZES} <= names
     assert {"math_slstm_zero", "math_slstm_nonzero", "math_slstm_mixed"} <= names
+    assert {f"bf16mma_{c}_wide" for c in SIZES} <= names
 
 
 # ------------------------------------------------------------ library known answers
