@@ -280,8 +280,10 @@ __device__ __forceinline__ uint32_t gather_mma(const Xchg& x, const int (&word)[
   bool first = true;
   using Op = Operand<MMA, SPLIT>;
   uint32_t spins = 0;
-  // A wave with no k-tiles (more compute waves than k-tiles: only where each
-  // wave has at most one, NF == 1) polls nothing but still does its between-work.
+  // A wave with no k-tiles (more compute waves than k-tiles) polls nothing but
+  // still does its between-work. Handled here where each wave has at most one
+  // k-tile (NF == 1); the GRU's backward at D = 32 (three k-tiles over four
+  // waves, NF = 3) keeps such a wave out of the gather itself.
   if constexpr (NF == 1) {
     if (nf <= 0) {
       zero();
@@ -462,8 +464,8 @@ __device__ __forceinline__ uint32_t gather_pair_mma(const Xchg& x, const int (&w
   // speculative: one chunk, multiplied while its tags are checked; otherwise
   // each chunk is multiplied once all of its tags are fresh
   constexpr bool kSpec = SPEC && NP <= PollChunk<MMA, NDT>::value;
-  // A wave with no k-tiles (more compute waves than k-tiles: only where each
-  // wave has at most one, NF == 1) polls nothing but still does its between-work.
+  // A wave with no k-tiles polls nothing but still does its between-work (see
+  // gather_mma for NF > 1).
   if constexpr (NF == 1) {
     if (nf <= 0) {
       zero();
@@ -1382,6 +1384,13 @@ __global__ void __launch_bounds__(64 * (KSC + 1) * NDT) bwd_kernel(BwdArgs a) {
   const int KT = p.kt_bwd;
   const int kt0 = (tm.kw * KT) / KS;
   const int nkt = ((tm.kw + 1) * KT) / KS - kt0;
+  // A wave without k-tiles (G_R*D/32 < KS: only the GRU, at D = 32, three
+  // k-tiles over four waves; the Elman's NF == 1 gather handles it) skips the
+  // gather, whose NF > 1 paths would also skip the prefetch of its next inputs;
+  // it adds a zero partial. (nkt is the same in every lane; read from the first
+  // lane, the branch stays a scalar one. The other cells keep the plain cut
+  // test: the extra condition measured 3% slower in the LSTM backward.)
+  const bool nopoll = cut || (CELL == CELL_GRU && __builtin_amdgcn_readfirstlane(nkt) <= 0);
 
   // ---- resident R^T: A[j][row = p][k = (o, g)] = R[g, n, o, dt*16 + row]
   Frag<MMA> A[NF];
@@ -1592,7 +1601,7 @@ __global__ void __launch_bounds__(64 * (KSC + 1) * NDT) bwd_kernel(BwdArgs a) {
         }
       }
     }
-    if (cut) {  // gradient_recurrent_cut: no R^T dG reaches h_{t-1}
+    if (nopoll) {  // gradient_recurrent_cut (no R^T dG reaches h_{t-1}), or no k-tiles
       zero();
       between();
     } else if (NB == 1 && pair) {
@@ -1604,7 +1613,7 @@ __global__ void __launch_bounds__(64 * (KSC + 1) * NDT) bwd_kernel(BwdArgs a) {
     }
     // paired split-word products: columns 8-15 hold the lo products of rows 0-7
     if constexpr (kSplit && NB == 1)
-      if (pair && !cut) acc[0] = fold_cols8(acc[0]);
+      if (pair && !nopoll) acc[0] = fold_cols8(acc[0]);
     prof.add(4, polls);
     prof.mark(0);
     prof.stamp(it, 2);
