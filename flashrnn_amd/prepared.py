@@ -25,7 +25,9 @@ accepted (the reference's prepared path has LSTM and sLSTM only), Wx has the
 cell's own gate count, inputs are BF16 or FP16 (recurrent product with 16-bit
 operands, FP32 accumulation and state -- the arithmetic of the reference's
 prepared kernels) or FP32 (FP32 product); the head width must be a multiple
-of 32 (at most 1024) because padding would break the fixed input addresses;
+of 16 from 16 to 1024 (as the reference requires a multiple of 16; widths that
+are not a multiple of 32 run on padded copies that every run refreshes from the
+caller's tensors, so in-place updates still reach the next run);
 ``config`` is this library's :class:`KernelConfig`, not the reference's
 kernel-family table (``execution_policy.py:11-60``), which names CUDA
 families that do not exist here.
@@ -86,8 +88,8 @@ class PreparedSequence:
         batch, steps, gates, heads, width = wx.shape
         if gates != gw or batch < 1 or steps < 1 or heads < 1:
             raise ValueError(f"expected nonempty B/T/H and {gw} gates for {cell}")
-        if width % 32 or not 32 <= width <= 1024:
-            raise ValueError("prepared execution needs D a multiple of 32, at most 1024")
+        if width % 16 or not 16 <= width <= 1024:
+            raise ValueError("prepared execution needs D >= 16, a multiple of 16, at most 1024")
         if recurrent.shape != (gr, heads, width, width) or bias.shape != (gt, heads, width):
             raise ValueError("invalid recurrent-weight or bias shape")
         if initial.shape != (S, batch, 1, heads, width):
@@ -118,12 +120,29 @@ class PreparedSequence:
         shape = (S, batch, steps, heads, width) if output_mode == "full" else (
             batch, 1 if output_mode == "last" else steps, heads, width)
         self.output = torch.empty(shape, dtype=dtype, device=dev)
+        # The kernels tile hidden units by 32. A width that is a multiple of 16
+        # only runs on zero-padded copies (inert units: zero weights, inputs and
+        # states), refreshed from the caller's tensors in every run; the
+        # outputs are copied back without the padding.
+        kw = width + (-width) % 32
+        self._padded = kw != width
+        if self._padded:
+            pad = lambda t, shp, dt=None: torch.zeros(shp, dtype=dt or t.dtype, device=dev)
+            self._wx = pad(wx, (batch, steps, gates, heads, kw))
+            self._recurrent = pad(recurrent, (gr, heads, kw, kw))
+            self._bias = pad(bias, (gt, heads, kw))
+            self._output = pad(self.output, shape[:-1] + (kw,))
+        else:
+            self._wx, self._recurrent, self._bias, self._output = wx, recurrent, bias, self.output
         # FP32 compute carries, alternating between chunks; an FP32 copy of a
         # lower-precision initial state (exact) is refreshed in every run
-        self.carries = tuple(torch.empty(initial.shape, dtype=torch.float32, device=dev) for _ in range(2))
+        cshape = initial.shape[:-1] + (kw,)
+        self.carries = tuple(torch.zeros(cshape, dtype=torch.float32, device=dev) for _ in range(2))
         self.final = self.carries[(len(lengths) - 1) % 2]
-        self.initial32 = None if initial.dtype == torch.float32 else torch.empty(
-            initial.shape, dtype=torch.float32, device=dev)
+        self.initial32 = None if initial.dtype == torch.float32 and not self._padded else torch.zeros(
+            cshape, dtype=torch.float32, device=dev)
+        if self._padded:
+            self.final = torch.empty(initial.shape, dtype=torch.float32, device=dev)
 
         exchange = config.exchange or ("shared" if _state["xcd_shared"] else "xcd")
         flags = _MODES[output_mode] | (_lib.FRNN_SNAPSHOT_F32 if dtype == torch.float32 else 0)
@@ -133,7 +152,7 @@ class PreparedSequence:
         lib = _lib.load()
         self._descs, start = [], 0
         for n in lengths:
-            d = _lib.FrnnDesc(_lib.CELLS[cell], batch, n, heads, width, _IO[wx.dtype], _lib.FRNN_F32, mma, flags,
+            d = _lib.FrnnDesc(_lib.CELLS[cell], batch, n, heads, kw, _IO[wx.dtype], _lib.FRNN_F32, mma, flags,
                               0.0, steps, start)
             if lib.frnn_workspace_bytes(d, 0) == 0:
                 raise ValueError(f"unsupported prepared configuration {cell} B{batch} T{n} N{heads} D{width}")
@@ -146,18 +165,26 @@ class PreparedSequence:
     def _execute(self):
         lib = _lib.load()
         stream = torch.cuda.current_stream(self.wx.device).cuda_stream
+        D = self.shape[3]
+        if self._padded:
+            self._wx[..., :D].copy_(self.wx)
+            self._recurrent[..., :D, :D].copy_(self.recurrent)
+            self._bias[..., :D].copy_(self.bias)
         previous = self.initial
         if self.initial32 is not None:
-            self.initial32.copy_(self.initial)
+            self.initial32[..., :D].copy_(self.initial)
             previous = self.initial32
         ws = self.workspace
         for index, d in enumerate(self._descs):
             carry = self.carries[index % 2]
-            rc = lib.frnn_fwd(d, self.wx.data_ptr(), self.recurrent.data_ptr(), self.bias.data_ptr(),
-                              previous.data_ptr(), self.output.data_ptr(), carry.data_ptr(), None,
+            rc = lib.frnn_fwd(d, self._wx.data_ptr(), self._recurrent.data_ptr(), self._bias.data_ptr(),
+                              previous.data_ptr(), self._output.data_ptr(), carry.data_ptr(), None,
                               ws.data_ptr(), ws.numel(), stream)
             _lib.check(rc, "frnn_fwd")
             previous = carry
+        if self._padded:
+            self.output.copy_(self._output[..., :D])
+            self.final.copy_(previous[..., :D])
         return self.output, self.final
 
     def check(self):

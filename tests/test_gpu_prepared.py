@@ -120,6 +120,48 @@ def test_graph_replay_tracks_input_updates():
         p.close()
 
 
+@pytest.mark.parametrize("cell,B,T,N,D", [("lstm", 5, 12, 2, 48), ("slstm", 3, 9, 1, 16), ("gru", 9, 10, 3, 80)],
+                         ids=["lstm-D48", "slstm-D16", "gru-D80"])
+def test_padded_width(cell, B, T, N, D):
+    """Widths that are a multiple of 16 but not of 32 run on padded copies:
+    bitwise flashrnn() (which pads the same way), in every policy, in chunks,
+    and under graph replay with the caller's tensors updated in place."""
+    from flashrnn_amd import flashrnn, set_strict
+    from flashrnn_amd.prepared import PreparedSequence
+
+    set_strict(True)
+    print(f"\n[prepared] padded width {cell} B{B} T{T} N{N} D{D}", flush=True)
+    args = inputs(cell, B, T, N, D, seed=28)
+    _, out, final = prepared(args, cell)
+    with torch.no_grad():
+        hist, last = flashrnn(*args, function=cell, dtype="bfloat16")
+    torch.cuda.synchronize()
+    assert out.shape == hist.shape and torch.equal(out, hist)
+    assert final.shape == last.shape and torch.equal(final, last)
+    _, ho, hf = prepared(args, cell, output_mode="hidden", chunks=[T // 2, T - T // 2])
+    assert torch.equal(ho, hist[0]) and torch.equal(hf, last)
+    _, lo, _ = prepared(args, cell, output_mode="last", snapshot_dtype=torch.float32)
+    assert lo.shape == (B, 1, N, D)
+    p = PreparedSequence(*args, cell, output_mode="full", chunks=[1, T - 1]).capture()
+    g = torch.Generator(device="cuda").manual_seed(6)
+    try:
+        for rep in range(3):
+            if rep:
+                args[0].copy_(torch.randn(args[0].shape, generator=g, device="cuda").to(args[0].dtype))
+                args[1].copy_((torch.randn(args[1].shape, generator=g, device="cuda") / D**0.5).to(args[1].dtype))
+            torch.cuda.synchronize()
+            o, f = p.run()
+            got = (o.clone(), f.clone())
+            torch.cuda.synchronize()
+            with torch.no_grad():
+                eo, ef = flashrnn(*args, function=cell, dtype="bfloat16")
+            torch.cuda.synchronize()
+            assert torch.equal(got[0], eo) and torch.equal(got[1], ef), rep
+        p.check()
+    finally:
+        p.close()
+
+
 def test_headline_head_shape_wide_and_bf16_initial():
     """The C2 head shape with a BF16 initial state (refreshed FP32 copy), and a two-tile (D = 768) head."""
     print("\n[prepared] lstm B8 T64 N3 D256 bf16 initial; gru B16 T12 N1 D768", flush=True)

@@ -29,8 +29,10 @@ def test_shape_errors():
     wx, R, b, s0 = args()
     with pytest.raises(ValueError, match="gates"):
         PreparedSequence(wx[:, :, :3], R, b, s0, "lstm")
-    with pytest.raises(ValueError, match="multiple of 32"):
-        PreparedSequence(*args(D=48), "lstm")
+    with pytest.raises(ValueError, match="multiple of 16"):
+        PreparedSequence(*args(D=40), "lstm")
+    with pytest.raises(ValueError, match="multiple of 16"):
+        PreparedSequence(*args(D=8), "lstm")
     with pytest.raises(ValueError, match="recurrent"):
         PreparedSequence(wx, R[:3], b, s0, "lstm")
     with pytest.raises(ValueError, match="initial"):
