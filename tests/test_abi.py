@@ -95,7 +95,8 @@ def test_unsupported_widths(lib, D):
         ("slstm", 576, "bf16", True), ("elman", 1024, "bf16", True), ("gru", 800, "bf16", False),
         ("lstm", 1024, "bf16", False), ("lstm", 512, "f32", True), ("gru", 768, "f32", False),
         ("elman", 768, "f32", True), ("lstm", 768, "f16", True), ("slstm", 256, "f16", True),
-        ("lstm", 1024, "f16", False),
+        ("lstm", 1024, "f16", False), ("elman", 1024, "f32", False), ("gru", 1024, "bf16", False),
+        ("slstm", 1024, "bf16", False),
     ],
 )
 def test_width_support(lib, cell, D, mma, ok):
