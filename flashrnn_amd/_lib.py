@@ -123,6 +123,17 @@ def strerror(code: int) -> str:
     return load().frnn_strerror(code).decode()
 
 
+class UnsupportedConfiguration(ValueError, RuntimeError):
+    """A shape, width or option mix the library has no kernel for.
+
+    A ``ValueError``, as the reference raises when no kernel configuration
+    solves its constraints (``flashrnn/flashrnn/cuda_init_parametric.py:25-65``;
+    its tests skip such sizes on ``ValueError``), and a ``RuntimeError`` like
+    every other failed call here."""
+
+
 def check(code: int, what: str) -> None:
+    if code == FRNN_E_UNSUPPORTED:
+        raise UnsupportedConfiguration(f"{what} failed: {strerror(code)} (code {code})")
     if code != FRNN_OK:
         raise RuntimeError(f"{what} failed: {strerror(code)} (code {code})")

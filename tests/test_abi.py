@@ -230,3 +230,16 @@ def test_shape_errors_and_cpu_tensors():
         flashrnn(wx, R, b, s0[:1], function="lstm")
     with pytest.raises(ValueError, match="device tensors"):
         flashrnn(wx, R, b, s0, function="lstm")
+
+
+def test_unsupported_configuration_is_a_value_error():
+    """The reference raises ValueError when no kernel configuration fits (its tests
+    skip such sizes on it); here FRNN_E_UNSUPPORTED does the same, and stays a
+    RuntimeError like every other failed call."""
+    with pytest.raises(ValueError, match="unsupported"):
+        _lib.check(_lib.FRNN_E_UNSUPPORTED, "frnn_fwd")
+    with pytest.raises(RuntimeError):
+        _lib.check(_lib.FRNN_E_UNSUPPORTED, "frnn_fwd")
+    with pytest.raises(RuntimeError) as e:
+        _lib.check(_lib.FRNN_E_TIMEOUT, "frnn_fwd")
+    assert not isinstance(e.value, ValueError)

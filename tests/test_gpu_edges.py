@@ -46,3 +46,21 @@ def test_edge_shapes(cell, B, T, N, D, dtype):
     print(errs, flush=True)
     for k, v in errs.items():
         assert v <= TOL[dtype], (k, v, errs)
+
+
+def test_unsupported_width_raises_value_error():
+    """LSTM D = 1024 has no kernel here: ValueError before anything runs, as the
+    reference raises when no configuration fits; the next call works."""
+    import torch
+
+    from flashrnn_amd import flashrnn, set_strict
+    from test_gpu_parity import make
+
+    set_strict(True)
+    cpu, _, _ = make("lstm", 2, 3, 1, 1024, seed=1)
+    with pytest.raises(ValueError, match="unsupported"):
+        flashrnn(*(t.cuda().bfloat16() for t in cpu), function="lstm", dtype="bfloat16")
+    actual, expected = run_pair("lstm", 2, 3, 1, 64, "bfloat16", seed=2)
+    for a, e in zip(actual, expected):
+        assert rel(a, e) <= TOL["bfloat16"]
+    torch.cuda.synchronize()
