@@ -45,6 +45,9 @@ def check(a, e):
 CASES = [
     ("lstm", 5, 9, 2, 64), ("lstm", 8, 48, 3, 256), ("gru", 3, 7, 2, 64), ("elman", 3, 7, 2, 32),
     ("slstm", 3, 7, 2, 64), ("gru", 16, 12, 1, 768), ("slstm", 16, 24, 2, 192),
+    # a backward wave without k-tiles (GRU D32), a two-tile LSTM over two
+    # batch slabs, the widest Elman
+    ("gru", 4, 6, 1, 32), ("lstm", 17, 5, 1, 640), ("elman", 20, 6, 2, 1024),
 ]
 
 
