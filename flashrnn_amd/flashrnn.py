@@ -63,7 +63,21 @@ class FlashRNNConfig:
     value, ``flashrnn.py:368-372``) and clamps the recurrent cotangent of
     ``h_{t-1}`` to the same interval before the caller's cotangent is added.
     ``forward_clipval`` is accepted and, as on the reference's fused backend,
-    has no effect."""
+    has no effect.
+
+    The caller-side layouts behave as in the reference (``flashrnn.py:162-170``,
+    permuted with ``permute_to`` at ``:97-108, 320-331``): ``input_shape``
+    (``"BTGHD"`` or ``"TBGHD"``), ``output_shape`` (any order of S, B, T, H, D;
+    default ``"SBTHD"``; the initial ``states`` argument and ``last`` use it
+    too, with T = 1), ``recurrent_shape`` (any order of G, H, D, P; default
+    ``"GHDP"``) and ``bias_shape`` (any order of G, H, D; default ``"GHD"``).
+    ``initial_val`` (a float or one per state) fills the initial state when
+    ``states`` is ``None`` (``_zero_state``, ``:930-957``). The other fields
+    of the reference's config are accepted for compatibility. ``constants``
+    must be empty (no cell here has any); ``dtype_acc`` must be FP32, the
+    accumulation type of every kernel. ``dtype_w`` / ``dtype_r`` /
+    ``dtype_b`` and the rest are informational: the tensors' own dtypes
+    decide (``io_dtype``)."""
 
     backend: str = "cuda_fused"
     function: str = "lstm"
@@ -71,9 +85,27 @@ class FlashRNNConfig:
     gradient_recurrent_cut: bool = False
     gradient_recurrent_clipval: Optional[float] = None
     forward_clipval: Optional[float] = None
+    constants: Optional[dict] = None
+    simple_agg: bool = True
+    hidden_dim: int = -1
     num_heads: int = -1
     head_dim: int = -1
     batch_size: int = -1
+    input_shape: str = "BTGHD"
+    output_shape: str = "SBTHD"
+    recurrent_shape: str = "GHDP"
+    bias_shape: str = "GHD"
+    dtype_acc: Optional[str] = "float32"
+    dtype_b: Optional[str] = None
+    dtype_r: Optional[str] = None
+    dtype_w: Optional[str] = None
+    dtype_g: Optional[str] = None
+    dtype_s: Optional[str] = None
+    dtype_a: Optional[str] = None
+    enable_automatic_mixed_precision: bool = True
+    trainable_r: object = True
+    trainable_b: object = True
+    initial_val: object = 0.0
 
     def __post_init__(self):
         if self.function not in CELL_SIZES:
@@ -89,6 +121,21 @@ class FlashRNNConfig:
         if v is not None and not (float(v) >= 0.0 and float(v) < float("inf")):
             raise ValueError(f"gradient_recurrent_clipval must be finite and >= 0, got {v}")
         (self.num_gates_r, self.num_gates_w, self.num_gates_t, self.num_states) = CELL_SIZES[self.function]
+        if self.input_shape not in ("BTGHD", "TBGHD"):
+            raise ValueError(f"input_shape must be 'BTGHD' or 'TBGHD', got {self.input_shape!r}")
+        for name, letters in (("output_shape", "SBTHD"), ("recurrent_shape", "GHDP"), ("bias_shape", "GHD")):
+            v = getattr(self, name)
+            if not isinstance(v, str) or sorted(v) != sorted(letters):
+                raise ValueError(f"{name} must order the letters {letters}, got {v!r}")
+        if self.constants:
+            raise ValueError(f"cell {self.function} has no constants, got {self.constants!r}")
+        self.constants = {}
+        self.simple_agg = self.function != "gru"  # the registry's value (flashrnn.py:45-70)
+        if self.dtype_acc not in (None, "float32"):
+            raise ValueError(f"dtype_acc must be float32 (every kernel accumulates in FP32), got {self.dtype_acc!r}")
+        iv = self.initial_val
+        if not isinstance(iv, (int, float)) and len(iv) != self.num_states:
+            raise ValueError(f"initial_val needs one value per state ({self.num_states}), got {iv!r}")
 
 
 # ----------------------------------------------------------------- status handling
@@ -266,6 +313,34 @@ def flashrnn(
     if config is None:
         config = FlashRNNConfig(backend=backend, function=function, dtype=dtype)
     cell = config.function
+    # caller-side layouts -> the kernels' [B,T,G,N,D], [G,N,D,P], [G,N,D], [S,B,T,N,D]
+    # (the reference's letters: H is the head index N here)
+    if config.input_shape != "BTGHD" and Wx.ndim == 5:
+        Wx = Wx.permute(_perm(config.input_shape, "BTGHD"))
+    if config.recurrent_shape != "GHDP" and R.ndim == 4:
+        R = R.permute(_perm(config.recurrent_shape, "GHDP"))
+    if config.bias_shape != "GHD" and b.ndim == 3:
+        b = b.permute(_perm(config.bias_shape, "GHD"))
+    if states is not None and config.output_shape != "SBTHD" and states.ndim == 5:
+        states = states.permute(_perm(config.output_shape, "SBTHD"))
+    if states is None and config.initial_val != 0.0 and Wx.ndim == 5:
+        S, (B, _, _, N, D) = CELL_SIZES[cell][3], Wx.shape
+        iv = config.initial_val
+        vals = [float(iv)] * S if isinstance(iv, (int, float)) else [float(v) for v in iv]
+        states = torch.tensor(vals, dtype=Wx.dtype, device=Wx.device).view(S, 1, 1, 1, 1).expand(S, B, 1, N, D)
+    hist, last = _flashrnn(Wx, R, b, states, cell, config)
+    if config.output_shape != "SBTHD":
+        p = _perm("SBTHD", config.output_shape)
+        hist, last = hist.permute(p), last.permute(p)
+    return hist, last
+
+
+def _perm(src: str, dst: str) -> tuple:
+    """Dimension order that takes layout ``src`` to ``dst`` (``permute_to``, flashrnn.py:97-108)."""
+    return tuple(src.index(x) for x in dst)
+
+
+def _flashrnn(Wx, R, b, states, cell, config):
     _check_shapes(cell, Wx, R, b, states)
     out_dtype = Wx.dtype
     io = io_dtype(Wx.dtype, R.dtype, b.dtype)
