@@ -74,7 +74,10 @@ struct Lds {
   static constexpr int NV = S + NSAVE;                      // staged values per element (forward)
   static constexpr int RING = GW * 64 * 4;                   // floats per Wx ring slot
   static constexpr int RED_F = 272 * 4;  // floats per (wave, batch tile), forward partials
-  static constexpr int RED_B = 304;      // floats per (batch tile, wave), backward partials
+  // floats per (batch tile, wave), backward partials: 304 used, padded to a
+  // multiple of 64 floats so the owners' KS reads of one element, RED_B apart,
+  // pair into ds_read2st64 (C2 backward 1.545 -> 1.53 ms)
+  static constexpr int RED_B = 320;
   static constexpr int XF = GW * NE;                         // floats per converted Wx slot
   __host__ __device__ static constexpr long fwd(int KS) {
     return 2L * KS * NB * RED_F + (long)kFwdRing * RING + 2L * NV * NE + (long)kFwdXf * XF;
