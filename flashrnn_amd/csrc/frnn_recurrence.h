@@ -1462,10 +1462,12 @@ __global__ void __launch_bounds__(64 * (KSC + 1) * NDT) bwd_kernel(BwdArgs a) {
   // Waves that own no element (KS > 4) start their poll late: polled at the
   // loop head, the exchange is stale, and the re-polls hold the CU's in-order
   // memory returns and the SIMDs the owners' pointwise runs on. Measured (LSTM
-  // backward): with at most 8 batch rows (paired polls) a fixed delay of ~500
-  // cycles is best (C2 1.61 -> 1.52 ms; waiting for the owners' flag in LDS
-  // 1.58 ms); with 16 rows waiting for the owners' flag, checked every ~250
-  // cycles, is (B16 N2 D384 3.81 -> 3.43 ms, N1 D512 4.53 -> 4.22 ms; the fixed
+  // backward): with at most 8 batch rows (paired polls) a fixed delay is best
+  // (C2 1.61 -> 1.52 ms; waiting for the owners' flag in LDS 1.58 ms). With the
+  // paired reduction reads, s_sleep 11 (~700 cycles) is best at C2: 1.525 ms
+  // at 8, 1.50 at 10, 1.487 at 11, 1.50 at 12, 1.54 at 13, 1.58 at 6 and at 16.
+  // With 16 rows, waiting for the owners' flag, checked every ~250 cycles, is
+  // best (B16 N2 D384 3.81 -> 3.43 ms, N1 D512 4.53 -> 4.22 ms; the fixed
   // delay 3.59 and 4.28 ms).
   constexpr int kOwnerWaves = (NE + 63) / 64 < KS ? (NE + 63) / 64 : KS;
   if (tm.kw == 0 && tm.lane < kOwnerWaves) pubf[tm.lane] = 0u;
@@ -1590,7 +1592,7 @@ __global__ void __launch_bounds__(64 * (KSC + 1) * NDT) bwd_kernel(BwdArgs a) {
     if constexpr (KS > kOwnerWaves) {
       if (tm.kw >= kOwnerWaves && !cut) {
         if (pair) {
-          __builtin_amdgcn_s_sleep(8);
+          __builtin_amdgcn_s_sleep(11);
         } else {
           // bounded: the owners raise their flags every iteration
           for (uint32_t w = 0; w < (1u << 20); ++w) {
