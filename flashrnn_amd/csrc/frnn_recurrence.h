@@ -1466,9 +1466,11 @@ __global__ void __launch_bounds__(64 * (KSC + 1) * NDT) bwd_kernel(BwdArgs a) {
   // (C2 1.61 -> 1.52 ms; waiting for the owners' flag in LDS 1.58 ms). With the
   // paired reduction reads, s_sleep 11 (~700 cycles) is best at C2: 1.525 ms
   // at 8, 1.50 at 10, 1.487 at 11, 1.50 at 12, 1.54 at 13, 1.58 at 6 and at 16.
-  // With 16 rows, waiting for the owners' flag, checked every ~250 cycles, is
-  // best (B16 N2 D384 3.81 -> 3.43 ms, N1 D512 4.53 -> 4.22 ms; the fixed
-  // delay 3.59 and 4.28 ms).
+  // With 16 rows, waiting for the owners' flag is best (B16 N2 D384 3.81 ->
+  // 3.43 ms, N1 D512 4.53 -> 4.22 ms; the fixed delay 3.59 and 4.28 ms),
+  // checked every ~130 cycles (s_sleep 2; against 4, B16 T1024 backward over
+  // two runs: D128 N6 1.78 -> 1.72 ms, D256 N3 2.26 -> 2.15-2.21, D384 N2 3.33
+  // -> 3.24-3.29, D512 N1 4.37 -> 4.29-4.33).
   constexpr int kOwnerWaves = (NE + 63) / 64 < KS ? (NE + 63) / 64 : KS;
   if (tm.kw == 0 && tm.lane < kOwnerWaves) pubf[tm.lane] = 0u;
   __builtin_amdgcn_s_waitcnt(0);  // no set-up load pending at the loop head (see the forward kernel)
@@ -1601,7 +1603,7 @@ __global__ void __launch_bounds__(64 * (KSC + 1) * NDT) bwd_kernel(BwdArgs a) {
             for (int k = 0; k < kOwnerWaves; ++k)
               pub &= __hip_atomic_load(pubf + k, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) > (uint32_t)it;
             if (pub) break;
-            __builtin_amdgcn_s_sleep(4);
+            __builtin_amdgcn_s_sleep(2);
           }
         }
       }
